@@ -1,0 +1,247 @@
+// Row-wise bandwidth kernels: dispatch gather, top-k combine, routing-weight
+// gradient gather, gated-activation backward. All are HBM-bound; each
+// wavefront owns one row and moves it with 16-byte vector loads/stores.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+// ---------------------------------------------------------------- errors
+static thread_local char g_err[512] = "";
+
+void mm_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int mm_check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    mm_set_error("%s: %s", what, hipGetErrorString(e));
+    return MM_E_LAUNCH;
+  }
+  return MM_OK;
+}
+
+extern "C" const char* mm_last_error(void) { return g_err; }
+extern "C" int mm_version(void) { return 1; }
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / 64;
+constexpr int kMaxGrid = 8192;
+
+struct alignas(16) Vec8 {
+  uint16_t h[8];
+};
+
+__device__ __forceinline__ void vec8_to_f32(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 f32_to_vec8(const float* f) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// out[i] = x[send_token[i]] for i < offsets[E].
+__global__ __launch_bounds__(kThreads) void permute_kernel(const uint4* __restrict__ x, int64_t ldx_v,
+                                                           const int32_t* __restrict__ send_token,
+                                                           const int32_t* __restrict__ offsets, int E,
+                                                           int hidden_v, uint4* __restrict__ out,
+                                                           int64_t ldo_v) {
+  const int nvalid = offsets[E];
+  const int lane = threadIdx.x & 63;
+  for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
+       row += gridDim.x * kRowsPerBlock) {
+    const uint4* src = x + static_cast<int64_t>(send_token[row]) * ldx_v;
+    uint4* dst = out + static_cast<int64_t>(row) * ldo_v;
+    for (int v = lane; v < hidden_v; v += 64) dst[v] = src[v];
+  }
+}
+
+// out[t] = bf16(sum_j fp32(y[route_to_send[t*k+j]])), slot order j = 0..k-1.
+__global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restrict__ y, int64_t ldy_v,
+                                                           const int32_t* __restrict__ route_to_send,
+                                                           int64_t T, int top_k, int hidden_v,
+                                                           uint4* __restrict__ out, int64_t ldo_v) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6); t < T;
+       t += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
+    const int my_row = lane < top_k ? route_to_send[t * top_k + lane] : -1;
+    uint4* dst = out + t * ldo_v;
+    for (int v = lane; v < hidden_v; v += 64) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < top_k; ++j) {
+        const int r = __shfl(my_row, j);
+        if (r >= 0) {
+          float f[8];
+          vec8_to_f32(y[static_cast<int64_t>(r) * ldy_v + v], f);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[q] += f[q];
+        }
+      }
+      dst[v] = f32_to_vec8(acc);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gather_route_grad_kernel(const uint16_t* __restrict__ dscale,
+                                                                     const int32_t* __restrict__ r2s,
+                                                                     int64_t R, float* __restrict__ g) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < R;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int r = r2s[i];
+    g[i] = r >= 0 ? bf16_bits_to_f32(dscale[r]) : 0.0f;
+  }
+}
+
+// Gated activation derivative pair (value, d/dgate, v(up), d/dup), as in
+// kernels/swiglu_bwd.py:52-83 of the reference.
+__device__ __forceinline__ void act_pair(int kind, float a, float b, float beta, float lbeta, float L,
+                                         float& act_a, float& dact_a, float& v, float& dv) {
+  if (kind == MM_ACT_SWIGLU) {
+    const float s = mm_sigmoid(a);
+    act_a = a * s;
+    dact_a = act_a * (1.0f - s) + s;
+    v = b;
+    dv = 1.0f;
+  } else if (kind == MM_ACT_CLAMP_SWIGLU) {
+    const float gc = fminf(a, L);
+    const float uc = fminf(fmaxf(b, -L), L);
+    const float s = mm_sigmoid(gc);
+    act_a = gc * s;
+    dact_a = (s + gc * s * (1.0f - s)) * (a <= L ? 1.0f : 0.0f);
+    v = uc;
+    dv = fabsf(b) <= L ? 1.0f : 0.0f;
+  } else {
+    const float t = mm_tanh(a / beta);
+    const float s = mm_sigmoid(a);
+    act_a = beta * t * s;
+    dact_a = (1.0f - t * t) * s + beta * t * s * (1.0f - s);
+    if (lbeta > 0.0f) {
+      const float tu = mm_tanh(b / lbeta);
+      v = lbeta * tu;
+      dv = 1.0f - tu * tu;
+    } else {
+      v = b;
+      dv = 1.0f;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
+    const uint4* __restrict__ ga, int64_t ld_ga_v, const uint4* __restrict__ fc1, int64_t ld_fc1_v,
+    const float* __restrict__ scale, const int32_t* __restrict__ offsets, int E, int inter_v, int kind,
+    float beta, float lbeta, float L, uint4* __restrict__ dab, uint16_t* __restrict__ dscale) {
+  const int nvalid = offsets[E];
+  const int lane = threadIdx.x & 63;
+  for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
+       row += gridDim.x * kRowsPerBlock) {
+    const float s = round_bf16(scale[row]);
+    const uint4* g_row = ga + static_cast<int64_t>(row) * ld_ga_v;
+    const uint4* a_row = fc1 + static_cast<int64_t>(row) * ld_fc1_v;
+    uint4* d_row = dab + static_cast<int64_t>(row) * ld_fc1_v;
+    float part = 0.0f;
+    for (int v = lane; v < inter_v; v += 64) {
+      float dc[8], a[8], b[8], da[8], db[8];
+      vec8_to_f32(g_row[v], dc);
+      vec8_to_f32(a_row[v], a);
+      vec8_to_f32(a_row[inter_v + v], b);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float act_a, dact_a, vv, dv;
+        act_pair(kind, a[q], b[q], beta, lbeta, L, act_a, dact_a, vv, dv);
+        da[q] = dc[q] * dact_a * vv * s;
+        db[q] = dc[q] * act_a * dv * s;
+        part += act_a * vv * dc[q];
+      }
+      d_row[v] = f32_to_vec8(da);
+      d_row[inter_v + v] = f32_to_vec8(db);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+    if (lane == 0) dscale[row] = f32_to_bf16_bits(part);
+  }
+}
+
+int grid_for_rows(int64_t rows) {
+  int64_t g = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (g < 1) g = 1;
+  if (g > kMaxGrid) g = kMaxGrid;
+  return static_cast<int>(g);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int mm_permute(const uint16_t* x, int64_t ldx, const int32_t* send_token, const int32_t* offsets,
+                          int32_t num_experts, int64_t max_rows, int32_t hidden, uint16_t* out, int64_t ldo,
+                          mm_stream_t stream) {
+  MM_CHECK_ARG(x && send_token && offsets && out, "mm_permute: null pointer");
+  MM_CHECK_ARG(num_experts > 0 && hidden > 0 && max_rows >= 0, "mm_permute: bad sizes");
+  MM_CHECK_ARG(hidden % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && aligned16(x) && aligned16(out),
+               "mm_permute: rows must be 16-byte aligned (hidden, strides multiple of 8)");
+  if (max_rows == 0) return MM_OK;
+  permute_kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
+      reinterpret_cast<const uint4*>(x), ldx / 8, send_token, offsets, num_experts, hidden / 8,
+      reinterpret_cast<uint4*>(out), ldo / 8);
+  return mm_check_launch("mm_permute");
+}
+
+extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_to_send, int64_t num_tokens,
+                          int32_t top_k, int32_t hidden, uint16_t* out, int64_t ldo, mm_stream_t stream) {
+  MM_CHECK_ARG(num_tokens >= 0 && hidden > 0, "mm_combine: bad sizes");
+  MM_CHECK_ARG(top_k > 0 && top_k <= 64, "mm_combine: top_k must be in [1, 64]");
+  if (num_tokens == 0) return MM_OK;
+  MM_CHECK_ARG(y && route_to_send && out, "mm_combine: null pointer");
+  MM_CHECK_ARG(hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) && aligned16(out),
+               "mm_combine: rows must be 16-byte aligned");
+  combine_kernel<<<grid_for_rows(num_tokens), kThreads, 0, mm_hip_stream(stream)>>>(
+      reinterpret_cast<const uint4*>(y), ldy / 8, route_to_send, num_tokens, top_k, hidden / 8,
+      reinterpret_cast<uint4*>(out), ldo / 8);
+  return mm_check_launch("mm_combine");
+}
+
+extern "C" int mm_gather_route_grad(const uint16_t* dscale, const int32_t* route_to_send, int64_t num_routes,
+                                    float* grad_rw, mm_stream_t stream) {
+  MM_CHECK_ARG(num_routes >= 0, "mm_gather_route_grad: bad size");
+  if (num_routes == 0) return MM_OK;
+  MM_CHECK_ARG(dscale && route_to_send && grad_rw, "mm_gather_route_grad: null pointer");
+  int64_t g = (num_routes + kThreads - 1) / kThreads;
+  if (g > kMaxGrid) g = kMaxGrid;
+  gather_route_grad_kernel<<<static_cast<int>(g), kThreads, 0, mm_hip_stream(stream)>>>(dscale, route_to_send,
+                                                                                        num_routes, grad_rw);
+  return mm_check_launch("mm_gather_route_grad");
+}
+
+extern "C" int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga, const uint16_t* fc1_out, int64_t ld_fc1,
+                             const float* scale, const int32_t* offsets, int32_t num_experts, int64_t max_rows,
+                             int32_t inter, int32_t act_kind, float situ_beta, float situ_linear_beta,
+                             float clamp_limit, uint16_t* dab, uint16_t* dscale, mm_stream_t stream) {
+  MM_CHECK_ARG(grad_act && fc1_out && scale && offsets && dab && dscale, "mm_swiglu_bwd: null pointer");
+  MM_CHECK_ARG(num_experts > 0 && inter > 0 && max_rows >= 0, "mm_swiglu_bwd: bad sizes");
+  MM_CHECK_ARG(inter % 8 == 0 && ld_ga % 8 == 0 && ld_fc1 % 8 == 0 && ld_fc1 >= 2 * inter && ld_ga >= inter,
+               "mm_swiglu_bwd: rows must be 16-byte aligned");
+  MM_CHECK_ARG(aligned16(grad_act) && aligned16(fc1_out) && aligned16(dab), "mm_swiglu_bwd: misaligned");
+  MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_swiglu_bwd: bad act_kind");
+  if (max_rows == 0) return MM_OK;
+  swiglu_bwd_kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
+      reinterpret_cast<const uint4*>(grad_act), ld_ga / 8, reinterpret_cast<const uint4*>(fc1_out), ld_fc1 / 8,
+      scale, offsets, num_experts, inter / 8, act_kind, situ_beta, situ_linear_beta, clamp_limit,
+      reinterpret_cast<uint4*>(dab), dscale);
+  return mm_check_launch("mm_swiglu_bwd");
+}

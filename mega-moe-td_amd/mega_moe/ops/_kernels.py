@@ -1,0 +1,132 @@
+"""Thin torch-facing wrappers over the libmegamoe C ABI.
+
+Each function allocates its outputs with torch (the C ABI itself never
+allocates), launches one entry point on the current stream, and returns the
+outputs. Shapes are checked here before any launch so a kernel never sees a
+grid or operand it does not expect.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_WS_CACHE: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
+    """Grow-only per-device byte workspace (reused across calls on one stream)."""
+    key = (str(device), tag)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = ws
+    return ws
+
+
+def _gemm_ws(device, max_rows: int, num_experts: int) -> torch.Tensor:
+    need = int(_lib.load().mm_gemm_workspace_bytes(max_rows, num_experts))
+    return workspace(device, need, "gemm")
+
+
+def _check_bf16(name: str, t: torch.Tensor):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be torch.bfloat16, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a HIP device tensor")
+
+
+def permute(x: torch.Tensor, send_token: torch.Tensor, offsets: torch.Tensor, max_rows: int) -> torch.Tensor:
+    """out[i] = x[send_token[i]] for the valid expert-major rows."""
+    _check_bf16("x", x)
+    hidden = x.shape[1]
+    out = torch.empty(max_rows, hidden, dtype=x.dtype, device=x.device)
+    _lib.call("mm_permute", _lib.ptr(x), x.stride(0), _lib.ptr(send_token), _lib.ptr(offsets),
+              offsets.numel() - 1, max_rows, hidden, _lib.ptr(out), out.stride(0), _lib.stream_of(x.device))
+    return out
+
+
+def fc1_swiglu(x, send_token, w1, offsets, weight_perm, max_rows: int, activation: str, situ_beta: float,
+               situ_linear_beta, clamp_limit: float, save_fc1: bool):
+    """FC1 grouped GEMM + weighted gated activation -> (act [rows, I], fc1_output [rows, 2I] | None)."""
+    _check_bf16("x", x)
+    _check_bf16("w1", w1)
+    num_experts, hidden, two_inter = w1.shape
+    inter = two_inter // 2
+    if x.shape[1] != hidden or not w1.is_contiguous() or x.stride(1) != 1:
+        raise ValueError("fc1_swiglu: x [*, H] and contiguous w1 [E, H, 2I] required")
+    dev = x.device
+    act = torch.empty(max_rows, inter, dtype=torch.bfloat16, device=dev)
+    fc1_out = torch.empty(max_rows, two_inter, dtype=torch.bfloat16, device=dev) if save_fc1 else None
+    ws = _gemm_ws(dev, max_rows, num_experts)
+    lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
+    _lib.call("mm_fc1_swiglu", _lib.ptr(x), x.stride(0), _lib.ptr(send_token), _lib.ptr(w1), _lib.ptr(offsets),
+              _lib.ptr(weight_perm), num_experts, max_rows, hidden, inter, _lib.ACT_KINDS[activation],
+              float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(act), _lib.ptr(fc1_out), _lib.ptr(ws),
+              ws.numel(), _lib.stream_of(dev))
+    return act, fc1_out
+
+
+def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_rows: int, n: int, k: int):
+    """c[i, :] = a[row(i), :] @ B_e for expert-major rows; B_e(k, n) = b[e*se + n*sn + k*sk]."""
+    _check_bf16("a", a)
+    _check_bf16("b", b)
+    if a.stride(1) != 1 or a.shape[1] != k:
+        raise ValueError("grouped_gemm: a must be [*, K] with unit column stride")
+    num_experts = offsets.numel() - 1
+    c = torch.empty(max_rows, n, dtype=torch.bfloat16, device=a.device)
+    ws = _gemm_ws(a.device, max_rows, num_experts)
+    _lib.call("mm_grouped_gemm", _lib.ptr(a), a.stride(0), _lib.ptr(a_rows), _lib.ptr(b), b_se, b_sn, b_sk,
+              _lib.ptr(offsets), num_experts, max_rows, n, k, _lib.ptr(c), c.stride(0), _lib.ptr(ws), ws.numel(),
+              _lib.stream_of(a.device))
+    return c
+
+
+def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int) -> torch.Tensor:
+    """c[e] = P_e^T Q_e over each expert's rows -> [E, n1, n2] bf16."""
+    _check_bf16("p", p)
+    _check_bf16("q", q)
+    if p.stride(1) != 1 or q.stride(1) != 1 or p.shape[1] != n1 or q.shape[1] != n2:
+        raise ValueError("grouped_wgrad: p [*, n1], q [*, n2] with unit column stride required")
+    num_experts = offsets.numel() - 1
+    c = torch.empty(num_experts, n1, n2, dtype=torch.bfloat16, device=p.device)
+    _lib.call("mm_grouped_wgrad", _lib.ptr(p), p.stride(0), _lib.ptr(p_rows), _lib.ptr(q), q.stride(0),
+              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, n1, n2, _lib.ptr(c), None, 0,
+              _lib.stream_of(p.device))
+    return c
+
+
+def combine(y, route_to_send, num_tokens: int, top_k: int) -> torch.Tensor:
+    """out[t] = bf16(sum_j fp32(y[route_to_send[t*k+j]])) (dropped routes skipped)."""
+    _check_bf16("y", y)
+    hidden = y.shape[1]
+    out = torch.empty(num_tokens, hidden, dtype=torch.bfloat16, device=y.device)
+    _lib.call("mm_combine", _lib.ptr(y), y.stride(0), _lib.ptr(route_to_send), num_tokens, top_k, hidden,
+              _lib.ptr(out), out.stride(0), _lib.stream_of(y.device))
+    return out
+
+
+def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str, situ_beta: float,
+               situ_linear_beta, clamp_limit: float):
+    """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16)."""
+    _check_bf16("grad_act", grad_act)
+    _check_bf16("fc1_out", fc1_out)
+    inter = fc1_out.shape[1] // 2
+    dev = fc1_out.device
+    dab = torch.empty(max_rows, 2 * inter, dtype=torch.bfloat16, device=dev)
+    dscale = torch.empty(max_rows, dtype=torch.bfloat16, device=dev)
+    lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
+    _lib.call("mm_swiglu_bwd", _lib.ptr(grad_act), grad_act.stride(0), _lib.ptr(fc1_out), fc1_out.stride(0),
+              _lib.ptr(scale), _lib.ptr(offsets), offsets.numel() - 1, max_rows, inter,
+              _lib.ACT_KINDS[activation], float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(dab),
+              _lib.ptr(dscale), _lib.stream_of(dev))
+    return dab, dscale
+
+
+def gather_route_grad(dscale, route_to_send, shape) -> torch.Tensor:
+    """grad_rw[r] = float(dscale[route_to_send[r]]), 0 for dropped routes."""
+    out = torch.empty(shape, dtype=torch.float32, device=dscale.device)
+    _lib.call("mm_gather_route_grad", _lib.ptr(dscale), _lib.ptr(route_to_send), out.numel(), _lib.ptr(out),
+              _lib.stream_of(dscale.device))
+    return out

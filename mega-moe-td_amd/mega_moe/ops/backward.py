@@ -1,0 +1,131 @@
+"""Five-stage MoE backward on one MI355X.
+
+Mirrors ``moe_backward_triton`` (src/mega_moe/ops/backward.py:100-399) and the
+hand-written reference backward it is checked against
+(tests/_moe_baselines.py:96-226). Given dy [T, H]:
+
+  1. FC2 dgrad   grad_act = gco @ down[e]      gco = dy[send_token] is gathered
+                                              inside the GEMM's A-tile load
+  2. SwiGLU bwd  dAB = [dGate | dUp], dscale   (mm_swiglu_bwd)
+  3. FC2 wgrad   dW2[e] = gco_e^T act_e        (mm_grouped_wgrad, rows gathered)
+  4. FC1 dgrad   dX = dAB @ W1[e]^T, then grad_hidden = top-k sum of dX and
+                 grad_routing_weights = dscale gathered to [T, k]
+  5. FC1 wgrad   dW1[e] = X_e^T dAB_e          (X rows re-gathered from
+                 hidden_states, written directly in the packed [E, H, 2I]
+                 gate_up layout)
+
+Returned keys follow the reference: grad_hidden, grad_routing_weights,
+grad_fc1_1 / grad_fc1_2 ([E, F, H] views), grad_fc2 ([E, H, F]) and the
+intermediates grad_swiglu, grad_fc1_output, grad_gate, grad_fc1; plus
+grad_gate_up, the packed [E, H, 2F] weight gradient.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..runtime.timing import NULL_TIMER
+from . import _kernels as K
+
+
+def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_states=None):
+    """Run the five backward stages on a ``saved`` dict from ``FusedMoEForward``.
+
+    ``peer_mem`` is accepted for signature compatibility (one GPU has no
+    symmetric buffer); ``grad_transport`` (MoonEP) must be ``None``.
+    """
+    if grad_transport is not None:
+        raise NotImplementedError("MoonEP replica gradient transport is not built")
+    if "fc1_output" not in saved:
+        raise ValueError("saved is missing fc1_output; run the forward with return_saved=True")
+    T = saved["batch_size"]
+    k = saved["topk"]
+    H = saved["hidden_dim"]
+    inter = saved["ffn_dim"]
+    R = saved["total_routes"]
+    w1 = saved["gate_up_weight"]
+    w2 = saved["down_weight"]
+    offsets = saved["split_size_cum_per_expert"]
+    send_token = saved["send_token_indices"]
+    r2s = saved["route_to_send"]
+    x = hidden_states if hidden_states is not None else saved["hidden_states"]
+    if dy.shape != (T, H):
+        raise ValueError(f"dy must have shape {(T, H)}, got {tuple(dy.shape)}")
+    dy = dy.to(torch.bfloat16).contiguous()
+    act_kw = dict(activation=saved["activation"], situ_beta=saved["situ_beta"],
+                  situ_linear_beta=saved["situ_linear_beta"], clamp_limit=saved["clamp_limit"])
+
+    tm = saved.get("_stage_timer") or NULL_TIMER
+    # step 1: FC2 dgrad, B_e(k=h, n=f) = down[e, h, f]
+    tm.begin("fc2_dgrad")
+    se, sh, sf = w2.stride()
+    grad_act = K.grouped_gemm(dy, send_token, w2, se, sf, sh, offsets, R, inter, H)
+    tm.end()
+    # step 2: gated-activation backward
+    tm.begin("swiglu_bwd")
+    dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R, **act_kw)
+    tm.end()
+    # step 3: FC2 wgrad  dW2[e][h, f] = sum_i gco[i, h] act[i, f]
+    tm.begin("fc2_wgrad")
+    grad_fc2 = K.grouped_wgrad(dy, send_token, saved["swiglu_out_weighted"], None, offsets, H, inter)
+    tm.end()
+    # step 4: FC1 dgrad, B_e(k=j, n=h) = W1[e, h, j]; top-k reduce; gate gather
+    tm.begin("fc1_dgrad")
+    dx = K.grouped_gemm(dab, None, w1, w1.stride(0), w1.stride(1), 1, offsets, R, H, 2 * inter)
+    tm.end()
+    tm.begin("combine_bwd")
+    grad_hidden = K.combine(dx, r2s, T, k)
+    grad_rw = K.gather_route_grad(dscale, r2s, (T, k))
+    tm.end()
+    # step 5: FC1 wgrad in the packed layout  dW1[e][h, j] = sum_i x[tok(i), h] dAB[i, j]
+    tm.begin("fc1_wgrad")
+    grad_gate_up = K.grouped_wgrad(x, send_token, dab, None, offsets, H, 2 * inter)
+    tm.end()
+
+    grad_fc1 = grad_gate_up.transpose(1, 2)  # [E, 2F, H] view
+    return dict(
+        grad_hidden=grad_hidden,
+        grad_routing_weights=grad_rw,
+        grad_fc1_1=grad_fc1[:, :inter],
+        grad_fc1_2=grad_fc1[:, inter:],
+        grad_fc2=grad_fc2,
+        grad_gate_up=grad_gate_up,
+        grad_swiglu=grad_act,
+        grad_fc1_output=dab,
+        grad_gate=dscale,
+        grad_fc1=grad_fc1,
+    )
+
+
+class MegaMoEBackwardFunction(torch.autograd.Function):
+    """Autograd function over unpacked weights (reference ops/backward.py:405-455).
+
+    Arguments: hidden_states [B, H], routing_weights [B, k] fp32,
+    selected_experts [B, k] int32, fc1_1 / fc1_2 [E, F, H], fc2 [E, H, F],
+    ep_group (None on one GPU), topk, peer_mem (unused placeholder).
+    """
+
+    @staticmethod
+    def forward(ctx, hidden_states, routing_weights, selected_experts, fc1_1, fc1_2, fc2, ep_group, topk,
+                peer_mem):
+        from .forward import FusedMoEForward, pack_gate_up_weights
+
+        E, F, H = fc1_1.shape
+        op = FusedMoEForward(ep_group, max_tokens_per_rank=max(1, hidden_states.shape[0]), hidden_size=H,
+                             top_k=topk, num_experts=E)
+        gate_up = pack_gate_up_weights(fc1_1, fc1_2)
+        with torch.no_grad():
+            output, saved = op.forward(hidden_states.contiguous(), selected_experts.contiguous(), gate_up, fc2,
+                                       routing_weights.contiguous(), return_saved=True)
+        ctx.saved = saved
+        ctx.inter = F
+        return output
+
+    @staticmethod
+    def backward(ctx, dy):
+        grads = moe_backward_triton(ctx.saved, dy)
+        return (grads["grad_hidden"], grads["grad_routing_weights"], None, grads["grad_fc1_1"],
+                grads["grad_fc1_2"], grads["grad_fc2"], None, None, None)
+
+
+__all__ = ["MegaMoEBackwardFunction", "moe_backward_triton"]

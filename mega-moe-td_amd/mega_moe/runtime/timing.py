@@ -1,0 +1,55 @@
+"""Per-stage HIP-event timing of the forward/backward pipeline.
+
+Plays the role of the reference's MOE_FWD_TIMING / MOE_BWD_STAGE_TIMING
+stage stamps (kernels/common.py:86-130, ops/backward.py:216-347): when a
+``StageTimer`` is attached to an operator, events are recorded on the launch
+stream between stages and ``summary()`` returns the mean milliseconds of each
+stage over the recorded passes. Without a timer nothing is recorded.
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+
+import torch
+
+
+class StageTimer:
+    def __init__(self):
+        self._events = []          # list of (name, start_event, end_event)
+        self._open = None
+
+    def begin(self, name: str):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self._open = (name, ev)
+
+    def end(self):
+        name, start = self._open
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self._events.append((name, start, ev))
+        self._open = None
+
+    def reset(self):
+        self._events.clear()
+
+    def summary(self) -> dict:
+        """Mean ms per stage name (synchronises)."""
+        torch.cuda.synchronize()
+        acc, cnt = defaultdict(float), defaultdict(int)
+        for name, a, b in self._events:
+            acc[name] += a.elapsed_time(b)
+            cnt[name] += 1
+        return {k: acc[k] / cnt[k] for k in acc}
+
+
+class _NullTimer:
+    def begin(self, name):
+        pass
+
+    def end(self):
+        pass
+
+
+NULL_TIMER = _NullTimer()

@@ -1,0 +1,272 @@
+"""CPU oracle of the Mega-MoE layer -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker or the timed CPU baseline. The
+product path (mega_moe) never calls it.
+
+A restatement, written for this repository, of the reference's algorithm:
+
+* routing     runtime/routing.py:621-671 (valid mask, float32 *stable*
+              argsort by expert id, token = route // k, histogram, exclusive
+              offsets) and kernels/fc2_combine.py:508-529 (inverse, -1 for
+              dropped routes) -- numpy, integer exact.
+* forward     tests/_moe_baselines.py:326-471 (torch_moe_fwd_golden) at one
+              rank: per-expert fp32 GEMMs of bf16 operands, gate and up
+              rounded to bf16, act = bf16(act_fn(gate, up) * w) with w in
+              fp32, FC2 rounded to bf16, combine = fp32 sum over the k slots in
+              slot order, rounded to bf16. The gated activation variants follow
+              ops/_torch_forward.py:177-205.
+* backward    tests/_moe_baselines.py:96-226 (moe_backward_torch) at one
+              rank, swiglu_bwd per tests/_moe_baselines.py:122-160 and
+              kernels/swiglu_bwd.py:52-83 (scale = the bf16-cast routing
+              weight, as the reference's saved recv_weights_sorted), every
+              GEMM output rounded to bf16 as the reference's bf16 matmuls are.
+
+Where each function is pinned (tests/test_oracle.py): routing against a
+pure-Python brute-force stable sort plus the reference's invariants
+(tests/function/test_single_kernel_stable_scatter.py); the forward against a
+per-token fp64 dense evaluation; combine with integer-valued rows (exact);
+the backward against torch.autograd of an fp64 restatement of the forward
+(as src/mega_moe/_goldens/backward.py:200-283 cross-checks it).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+ACTIVATIONS = ("swiglu", "situglu", "clamp_swiglu")
+
+
+def bf16(t: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 (RNE) and return as fp32."""
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+# --------------------------------------------------------------------- routing
+def route(selected: np.ndarray, num_experts: int, top_k: int) -> dict:
+    """Stable expert-major routing tables (runtime/routing.py:621-671)."""
+    flat = np.asarray(selected, dtype=np.int64).reshape(-1)
+    valid = (flat >= 0) & (flat < num_experts)
+    kept = np.nonzero(valid)[0]
+    order = np.argsort(flat[kept].astype(np.float32), kind="stable")
+    send_route = kept[order].astype(np.int32)
+    counts = np.bincount(flat[kept], minlength=num_experts).astype(np.int32)
+    offsets = np.zeros(num_experts + 1, dtype=np.int32)
+    offsets[1:] = np.cumsum(counts)
+    route_to_send = np.full(flat.shape[0], -1, dtype=np.int32)
+    route_to_send[send_route] = np.arange(send_route.shape[0], dtype=np.int32)
+    return dict(
+        send_route=send_route,
+        send_token=(send_route // top_k).astype(np.int32),
+        counts=counts,
+        offsets=offsets,
+        route_to_send=route_to_send,
+        stable_sort_indices=order.astype(np.int64),
+        valid=valid,
+    )
+
+
+# --------------------------------------------------------------------- activation
+def gated_act(g, u, activation="swiglu", situ_beta=1.0, situ_linear_beta=None, clamp_limit=7.0):
+    """act(gate) * v(up) in the input precision (ops/_torch_forward.py:177-205)."""
+    if activation == "swiglu":
+        return torch.nn.functional.silu(g) * u
+    if activation == "clamp_swiglu":
+        return torch.nn.functional.silu(g.clamp(max=clamp_limit)) * u.clamp(min=-clamp_limit, max=clamp_limit)
+    if activation == "situglu":
+        a = situ_beta * torch.tanh(g / situ_beta) * torch.sigmoid(g)
+        if situ_linear_beta is not None:
+            u = situ_linear_beta * torch.tanh(u / situ_linear_beta)
+        return a * u
+    raise ValueError(activation)
+
+
+def gated_act_grad(g, u, activation="swiglu", situ_beta=1.0, situ_linear_beta=None, clamp_limit=7.0):
+    """(act_a, dact_a, v, dv) per tests/_moe_baselines.py:122-160 and kernels/swiglu_bwd.py:52-83."""
+    if activation == "swiglu":
+        s = torch.sigmoid(g)
+        act_a = g * s
+        return act_a, act_a * (1 - s) + s, u, torch.ones_like(u)
+    if activation == "clamp_swiglu":
+        L = clamp_limit
+        gc = g.clamp(max=L)
+        s = torch.sigmoid(gc)
+        act_a = gc * s
+        dact = (s + gc * s * (1 - s)) * (g <= L).to(g.dtype)
+        return act_a, dact, u.clamp(min=-L, max=L), (u.abs() <= L).to(u.dtype)
+    t = torch.tanh(g / situ_beta)
+    s = torch.sigmoid(g)
+    act_a = situ_beta * t * s
+    dact = (1 - t * t) * s + situ_beta * t * s * (1 - s)
+    if situ_linear_beta is not None:
+        tu = torch.tanh(u / situ_linear_beta)
+        return act_a, dact, situ_linear_beta * tu, 1 - tu * tu
+    return act_a, dact, u, torch.ones_like(u)
+
+
+# --------------------------------------------------------------------- forward
+def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, situ_linear_beta=None,
+            clamp_limit=7.0):
+    """Layer forward on CPU.
+
+    x [T, H] bf16; selected [T, k] int32; gate_up [E, H, 2I] bf16;
+    down [E, H, I] bf16 (any strides); rw [T, k] fp32.
+    Returns (out [T, H] bf16, state dict for ``backward``).
+    """
+    T, H = x.shape
+    k = selected.shape[1]
+    E, _, two_i = gate_up.shape
+    inter = two_i // 2
+    tb = route(selected.cpu().numpy(), E, k)
+    send_token = torch.from_numpy(tb["send_token"]).long()
+    send_route = torch.from_numpy(tb["send_route"]).long()
+    offsets = tb["offsets"]
+    xf = x.float().cpu()
+    w1 = gate_up.float().cpu()
+    w2 = down.float().cpu()
+    wp = rw.float().cpu().reshape(-1)[send_route]
+    M = send_route.numel()
+    gate = torch.empty(M, inter)
+    up = torch.empty(M, inter)
+    y = torch.empty(M, H)
+    xp = xf[send_token]
+    for e in range(E):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if a == b:
+            continue
+        gu = xp[a:b] @ w1[e]
+        gate[a:b] = bf16(gu[:, :inter])
+        up[a:b] = bf16(gu[:, inter:])
+    act = bf16(gated_act(gate, up, activation, situ_beta, situ_linear_beta, clamp_limit) * wp[:, None])
+    for e in range(E):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if a == b:
+            continue
+        y[a:b] = bf16(act[a:b] @ w2[e].T)
+    r2s = torch.from_numpy(tb["route_to_send"]).long().view(T, k)
+    out = torch.zeros(T, H)
+    for j in range(k):
+        rows = r2s[:, j]
+        m = rows >= 0
+        out[m] += y[rows[m]]
+    state = dict(tables=tb, x=xf, w1=w1, w2=w2, wp=wp, gate=gate, up=up, act=act, y=y, T=T, k=k, E=E,
+                 inter=inter, activation=activation, situ_beta=situ_beta, situ_linear_beta=situ_linear_beta,
+                 clamp_limit=clamp_limit)
+    return out.to(torch.bfloat16), state
+
+
+def forward_tokens(x, selected, gate_up, down, rw, tokens, activation="swiglu", situ_beta=1.0,
+                   situ_linear_beta=None, clamp_limit=7.0):
+    """Forward output rows for a subset of tokens only (same rounding points).
+
+    Lets a test check full-size configurations on sampled tokens.
+    """
+    E, H, two_i = gate_up.shape
+    inter = two_i // 2
+    k = selected.shape[1]
+    rows = []
+    for t in tokens:
+        acc = torch.zeros(H)
+        xt = x[t].float().cpu()
+        for j in range(k):
+            e = int(selected[t, j])
+            if not 0 <= e < E:
+                continue
+            gu = xt @ gate_up[e].float().cpu()
+            g, u = bf16(gu[:inter]), bf16(gu[inter:])
+            a = bf16(gated_act(g, u, activation, situ_beta, situ_linear_beta, clamp_limit) * float(rw[t, j]))
+            acc += bf16(down[e].float().cpu() @ a)
+        rows.append(acc.to(torch.bfloat16))
+    return torch.stack(rows)
+
+
+# --------------------------------------------------------------------- backward
+def backward(state, dy):
+    """Five-stage backward on CPU (tests/_moe_baselines.py:96-226)."""
+    tb = state["tables"]
+    T, k, E, inter = state["T"], state["k"], state["E"], state["inter"]
+    offsets = tb["offsets"]
+    send_token = torch.from_numpy(tb["send_token"]).long()
+    w1, w2 = state["w1"], state["w2"]
+    dyf = dy.float().cpu()
+    H = dyf.shape[1]
+    gco = bf16(dyf)[send_token]                                   # step 1a
+    M = gco.shape[0]
+    grad_act = torch.empty(M, inter)
+    for e in range(E):                                            # step 1b
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if a < b:
+            grad_act[a:b] = bf16(gco[a:b] @ w2[e])
+    scale = bf16(state["wp"])[:, None]                            # step 2
+    act_a, dact, v, dv = gated_act_grad(state["gate"], state["up"], state["activation"], state["situ_beta"],
+                                        state["situ_linear_beta"], state["clamp_limit"])
+    dgate = grad_act * dact * v * scale
+    dup = grad_act * act_a * dv * scale
+    dab = bf16(torch.cat([dgate, dup], dim=1))
+    dscale = bf16((act_a * v * grad_act).sum(dim=1))
+    grad_fc2 = torch.zeros(E, H, inter)                           # step 3
+    dx = torch.empty(M, H)
+    grad_gate_up = torch.zeros(E, H, 2 * inter)
+    xp = state["x"][send_token]
+    for e in range(E):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        if a == b:
+            continue
+        grad_fc2[e] = bf16(gco[a:b].T @ state["act"][a:b])
+        dx[a:b] = bf16(dab[a:b] @ w1[e].T)                        # step 4a
+        grad_gate_up[e] = bf16(xp[a:b].T @ dab[a:b])              # step 5
+    r2s = torch.from_numpy(tb["route_to_send"]).long().view(T, k)
+    grad_hidden = torch.zeros(T, H)                               # step 4b
+    grad_rw = torch.zeros(T, k)
+    for j in range(k):
+        rows = r2s[:, j]
+        m = rows >= 0
+        grad_hidden[m] += dx[rows[m]]
+        grad_rw[m, j] = dscale[rows[m]]
+    return dict(
+        grad_hidden=grad_hidden.to(torch.bfloat16),
+        grad_routing_weights=grad_rw,
+        grad_fc2=grad_fc2.to(torch.bfloat16),
+        grad_gate_up=grad_gate_up.to(torch.bfloat16),
+        grad_swiglu=grad_act,
+        grad_fc1_output=dab,
+        grad_gate=dscale,
+    )
+
+
+# --------------------------------------------------------------------- fp64 autograd restatement
+def reference_autograd(x, selected, gate_up, down, rw, dy, activation="swiglu", situ_beta=1.0,
+                       situ_linear_beta=None, clamp_limit=7.0):
+    """Dense per-token fp64 forward + torch.autograd gradients (no rounding).
+
+    Independent of ``route``: each token loops over its own k slots. Used to
+    pin ``forward`` and ``backward`` against the calculus, not against
+    themselves. The only rounding kept is gate/up -> bf16 (value only), so the
+    piecewise clamp derivative is taken on the same side as in the oracle.
+    """
+    xd = x.double().cpu().clone().requires_grad_(True)
+    rwd = rw.double().cpu().clone().requires_grad_(True)
+    w1 = gate_up.double().cpu().clone().requires_grad_(True)
+    w2 = down.double().cpu().clone().requires_grad_(True)
+    T, k = selected.shape
+    E, H, two_i = gate_up.shape
+    inter = two_i // 2
+    outs = []
+    for t in range(T):
+        acc = torch.zeros(H, dtype=torch.float64)
+        for j in range(k):
+            e = int(selected[t, j])
+            if not 0 <= e < E:
+                continue
+            gu = xd[t] @ w1[e]
+            # evaluate act and its derivative at the bf16-rounded gate/up, as
+            # the reference does (straight-through: value rounded, gradient 1)
+            gu = gu + (gu.to(torch.bfloat16).double() - gu).detach()
+            a = gated_act(gu[:inter], gu[inter:], activation, situ_beta, situ_linear_beta, clamp_limit) * rwd[t, j]
+            acc = acc + w2[e] @ a
+        outs.append(acc)
+    out = torch.stack(outs)
+    out.backward(dy.double().cpu())
+    return dict(out=out.detach(), grad_hidden=xd.grad, grad_routing_weights=rwd.grad, grad_gate_up=w1.grad,
+                grad_fc2=w2.grad)

@@ -1,0 +1,44 @@
+"""The C-ABI library loads and exports every symbol include/megamoe.h declares
+(no compute calls: runs without a GPU)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mega_moe import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "megamoe.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("mm_route", "mm_fc1_swiglu", "mm_grouped_gemm", "mm_grouped_wgrad", "mm_combine", "mm_swiglu_bwd",
+              "mm_permute", "mm_gather_route_grad", "mm_last_error"):
+        assert s in syms
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.library_path()), reason="libmegamoe.so not built")
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.library_path())
+    for s in declared_symbols():
+        assert hasattr(lib, s), f"libmegamoe.so does not export {s}"
+        assert s in _lib.SIGNATURES, f"python binding lacks a prototype for {s}"
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.library_path()), reason="libmegamoe.so not built")
+def test_host_side_argument_errors():
+    # Argument validation runs on the host and never touches a device.
+    lib = _lib.load()
+    rc = lib.mm_route(None, 10, 2, 0, None, None, None, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"num_experts" in lib.mm_last_error()
+    rc = lib.mm_grouped_gemm(None, 0, None, None, 0, 0, 0, None, 1, 1, 100, 64, None, 0, None, 0, None)
+    assert rc == -1
+    assert lib.mm_route_workspace_bytes(131072, 896) >= 64 * 896 * 4

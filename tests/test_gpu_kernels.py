@@ -1,0 +1,205 @@
+"""Parity of each HIP entry point against the CPU oracle / fp32 torch (GPU)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests._numeric import assert_rel
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _route_gpu(sel, E, rw=None):
+    from mega_moe.ops import _kernels as K
+    from mega_moe.runtime.routing import route
+    from mega_moe import _lib
+    need = int(_lib.load().mm_route_workspace_bytes(sel.numel(), E))
+    ws = K.workspace(sel.device, need, "route")
+    t = route(sel, E, rw, ws)
+    torch.cuda.synchronize()
+    return t
+
+
+ROUTE_CASES = [
+    # (T, k, E, pattern)
+    (0, 2, 8, "uniform"),
+    (1, 1, 1, "uniform"),
+    (512, 2, 8, "uniform"),
+    (333, 3, 7, "drops"),
+    (1000, 4, 64, "hot"),
+    (4096, 8, 32, "uniform"),
+    (4096, 16, 896, "uniform"),
+    (8192, 8, 128, "drops"),
+    (16384, 8, 32, "zipf"),
+    (2049, 5, 1024, "drops"),
+]
+
+
+def _make_sel(T, k, E, pattern, seed):
+    rng = np.random.default_rng(seed)
+    if pattern == "hot":
+        sel = np.zeros((T, k), np.int32)
+        sel[:, 1:] = rng.integers(0, E, size=(T, k - 1))
+    elif pattern == "zipf":
+        p = (np.arange(E) + 1.0) ** -1.2
+        p /= p.sum()
+        sel = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32) \
+            if T else np.zeros((0, k), np.int32)
+    else:
+        sel = rng.integers(0, E, size=(T, k)).astype(np.int32)
+    if pattern == "drops" and T:
+        m = rng.random((T, k)) < 0.2
+        sel[m] = rng.choice([-1, E, E + 7, -100], size=int(m.sum()))
+    return sel
+
+
+@pytest.mark.parametrize("T,k,E,pattern", ROUTE_CASES)
+def test_route_bit_exact(T, k, E, pattern):
+    sel_np = _make_sel(T, k, E, pattern, seed=T + E)
+    sel = torch.from_numpy(sel_np).to(DEV)
+    rw = torch.rand(T, k, device=DEV)
+    t = _route_gpu(sel, E, rw)
+    ref = O.route(sel_np, E, k)
+    nv = int(ref["offsets"][-1])
+    assert t.offsets.cpu().numpy().tolist() == ref["offsets"].tolist()
+    assert t.counts.cpu().numpy().tolist() == ref["counts"].tolist()
+    assert np.array_equal(t.send_route[:nv].cpu().numpy(), ref["send_route"])
+    assert np.array_equal(t.send_token[:nv].cpu().numpy(), ref["send_token"])
+    assert np.array_equal(t.route_to_send.cpu().numpy(), ref["route_to_send"])
+    wp = rw.reshape(-1)[torch.from_numpy(ref["send_route"]).long().to(DEV)]
+    assert torch.equal(t.weight_perm[:nv], wp)
+
+
+def _ragged(E, counts_kind, seed, total=None):
+    rng = np.random.default_rng(seed)
+    if counts_kind == "balanced":
+        c = np.full(E, 100)
+    elif counts_kind == "ragged":
+        c = rng.integers(0, 300, size=E)
+        c[0] = 0
+        c[-1] = 1
+    else:  # skew
+        c = (2000 / (np.arange(E) + 1) ** 1.2).astype(int)
+    offs = np.zeros(E + 1, np.int32)
+    offs[1:] = np.cumsum(c)
+    return torch.from_numpy(offs).to(DEV)
+
+
+def _ref_rows_gemm(a, a_rows, bmat, offs):
+    """fp32 reference: c[i] = a[row(i)] @ bmat[e] with bmat[e] [K, N]."""
+    offs = offs.cpu().tolist()
+    af = a.float().cpu()
+    if a_rows is not None:
+        af = af[a_rows.long().cpu()]
+    out = torch.zeros(offs[-1], bmat.shape[2])
+    for e in range(len(offs) - 1):
+        if offs[e + 1] > offs[e]:
+            out[offs[e]:offs[e + 1]] = af[offs[e]:offs[e + 1]] @ bmat[e].float().cpu()
+    return out
+
+
+@pytest.mark.parametrize("layout", ["kcontig", "ncontig"])
+@pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
+@pytest.mark.parametrize("gather", [False, True])
+def test_grouped_gemm(layout, kind, gather):
+    from mega_moe.ops import _kernels as K
+    E, N, Kd = 6, 256, 192
+    offs = _ragged(E, kind, seed=3)
+    M = int(offs[-1])
+    g = torch.Generator(device=DEV).manual_seed(0)
+    src_rows = M + 17
+    a = torch.randn(src_rows, Kd, device=DEV, generator=g).to(torch.bfloat16)
+    a_rows = torch.randint(0, src_rows, (M,), device=DEV, dtype=torch.int32, generator=g) if gather else None
+    if not gather:
+        a = a[:M]
+    if layout == "kcontig":
+        bt = torch.randn(E, N, Kd, device=DEV, generator=g).to(torch.bfloat16)  # B_e(k, n) = bt[e, n, k]
+        c = K.grouped_gemm(a, a_rows, bt, bt.stride(0), bt.stride(1), bt.stride(2), offs, M, N, Kd)
+        bmat = bt.transpose(1, 2)
+    else:
+        bm = torch.randn(E, Kd, N, device=DEV, generator=g).to(torch.bfloat16)  # B_e(k, n) = bm[e, k, n]
+        c = K.grouped_gemm(a, a_rows, bm, bm.stride(0), bm.stride(2), bm.stride(1), offs, M, N, Kd)
+        bmat = bm
+    torch.cuda.synchronize()
+    ref = _ref_rows_gemm(a, a_rows, bmat, offs)
+    assert_rel(c[:M], ref, 1e-2, "grouped_gemm")
+
+
+@pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
+@pytest.mark.parametrize("gather", [False, True])
+def test_grouped_wgrad(kind, gather):
+    from mega_moe.ops import _kernels as K
+    E, N1, N2 = 5, 256, 128
+    offs = _ragged(E, kind, seed=4)
+    M = int(offs[-1])
+    g = torch.Generator(device=DEV).manual_seed(1)
+    p = torch.randn(M + 9, N1, device=DEV, generator=g).to(torch.bfloat16)
+    q = torch.randn(M, N2, device=DEV, generator=g).to(torch.bfloat16)
+    p_rows = torch.randint(0, M + 9, (M,), device=DEV, dtype=torch.int32, generator=g) if gather else None
+    c = K.grouped_wgrad(p, p_rows, q, None, offs, N1, N2)
+    torch.cuda.synchronize()
+    pf = p.float().cpu()
+    pf = pf[p_rows.long().cpu()] if gather else pf[:M]
+    qf = q.float().cpu()
+    o = offs.cpu().tolist()
+    ref = torch.zeros(E, N1, N2)
+    for e in range(E):
+        ref[e] = pf[o[e]:o[e + 1]].T @ qf[o[e]:o[e + 1]]
+    assert_rel(c, ref, 1e-2, "grouped_wgrad")
+    for e in range(E):
+        if o[e + 1] == o[e]:
+            assert torch.count_nonzero(c[e]) == 0
+
+
+def test_combine_integer_exact():
+    from mega_moe.ops import _kernels as K
+    T, k, H = 300, 6, 384
+    rows = T * k
+    y = (torch.arange(rows * H, device=DEV) % 23 - 11).to(torch.bfloat16).view(rows, H)
+    perm = torch.randperm(rows, device=DEV).to(torch.int32)
+    perm[::7] = -1
+    out = K.combine(y, perm, T, k)
+    torch.cuda.synchronize()
+    yf = y.float().cpu()
+    p = perm.view(T, k).long().cpu()
+    ref = torch.zeros(T, H)
+    for j in range(k):
+        m = p[:, j] >= 0
+        ref[m] += yf[p[m, j]]
+    assert torch.equal(out.float().cpu(), ref)
+
+
+def test_permute_exact():
+    from mega_moe.ops import _kernels as K
+    x = torch.randn(100, 256, device=DEV).to(torch.bfloat16)
+    st = torch.randint(0, 100, (400,), device=DEV, dtype=torch.int32)
+    offs = torch.tensor([0, 150, 150, 390], dtype=torch.int32, device=DEV)
+    out = K.permute(x, st, offs, 400)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:390], x[st[:390].long()])
+
+
+@pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu", "situglu"])
+def test_swiglu_bwd(activation):
+    from mega_moe.ops import _kernels as K
+    M, inter = 300, 256
+    g = torch.Generator(device=DEV).manual_seed(5)
+    fc1 = torch.randn(M, 2 * inter, device=DEV, generator=g).to(torch.bfloat16)
+    ga = torch.randn(M, inter, device=DEV, generator=g).to(torch.bfloat16)
+    sc = torch.rand(M, device=DEV, generator=g)
+    offs = torch.tensor([0, 100, 290], dtype=torch.int32, device=DEV)
+    kw = dict(activation=activation, situ_beta=1.5, situ_linear_beta=2.0 if activation == "situglu" else None,
+              clamp_limit=0.5)
+    dab, ds = K.swiglu_bwd(ga, fc1, sc, offs, M, **kw)
+    torch.cuda.synchronize()
+    gate, up = fc1[:290, :inter].float().cpu(), fc1[:290, inter:].float().cpu()
+    act_a, dact, v, dv = O.gated_act_grad(gate, up, **kw)
+    s = O.bf16(sc[:290].cpu())[:, None]
+    gaf = ga[:290].float().cpu()
+    ref_dab = torch.cat([gaf * dact * v * s, gaf * act_a * dv * s], 1)
+    ref_ds = (act_a * v * gaf).sum(1)
+    assert_rel(dab[:290], ref_dab, 1e-2, "dab")
+    assert_rel(ds[:290], ref_ds, 1e-2, "dscale")

@@ -1,0 +1,127 @@
+"""Layer-level parity: FusedMoEForward / moe_backward_triton / MegaMoEFunction
+against the CPU oracle (GPU)."""
+
+import pytest
+import torch
+
+import mega_moe
+from mega_moe.bench_configs import CASES, CaseSpec, make_inputs
+from oracle import moe_oracle as O
+from tests._numeric import GRAD_ATOL, GRAD_RTOL, OUTPUT_ATOL, OUTPUT_RTOL, assert_rel, cmp_grad
+
+pytestmark = pytest.mark.gpu
+
+SMALL = [
+    CaseSpec("small_topk", 256, 256, 128, 8, 4, "softmax_topk", True),
+    CaseSpec("small_skew", 384, 256, 256, 16, 4, "zipf", True),
+    CaseSpec("toy_bf16", 512, 256, 512, 8, 2, "softmax_topk", True),
+]
+
+
+def _op(spec, activation="swiglu", **cfg):
+    config = mega_moe.MoEForwardConfig(activation=activation, **cfg)
+    return mega_moe.FusedMoEForward(None, max_tokens_per_rank=spec.tokens, hidden_size=spec.hidden,
+                                    top_k=spec.top_k, num_experts=spec.experts, config=config)
+
+
+def _act_kw(activation):
+    return dict(activation=activation, situ_beta=1.0 if activation != "situglu" else 2.0,
+                situ_linear_beta=3.0 if activation == "situglu" else None,
+                clamp_limit=7.0 if activation != "clamp_swiglu" else 0.05)
+
+
+@pytest.mark.parametrize("spec", SMALL, ids=lambda s: s.name)
+@pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu", "situglu"])
+def test_forward_backward_parity(spec, activation):
+    inp = make_inputs(spec, device="cuda", seed=7, weight_scale=0.1)
+    sel = inp["selected"].clone()
+    sel[0, 0] = -1                      # dropped routes (reference drop_frac cases)
+    sel[5, 1] = spec.experts
+    kw = _act_kw(activation)
+    cfg = {k: v for k, v in kw.items() if k != "activation"}
+    op = _op(spec, activation, **cfg)
+    out, saved = op.forward(inp["x"], sel, inp["gate_up"], inp["down"], inp["rw"], return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, inp["dy"], peer_mem=None)
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), sel.cpu(), inp["gate_up"].cpu(), inp["down"].cpu(),
+                            inp["rw"].cpu(), **kw)
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out, ref_out, 2e-2, "output")
+    torch.testing.assert_close(out.float().cpu(), ref_out.float(), rtol=OUTPUT_RTOL, atol=OUTPUT_ATOL)
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
+        assert_rel(g[name], ref[name], 2e-2, name)
+        assert cmp_grad(g[name], ref[name], GRAD_RTOL, GRAD_ATOL) == 0, name
+    assert g["grad_routing_weights"][0, 0] == 0 and g["grad_routing_weights"][5, 1] == 0
+    # unpacked views follow the reference's [E, F, H] layout
+    I = spec.inter
+    assert torch.equal(g["grad_fc1_1"], g["grad_gate_up"][:, :, :I].transpose(1, 2))
+
+
+def test_routing_plan_and_dispatch_fc1():
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=3)
+    op = _op(spec)
+    sel = inp["selected"]
+    plan = op.build_routing_plan(sel)
+    ref = O.route(sel.cpu().numpy(), spec.experts, spec.top_k)
+    assert plan.num_received_routes == int(ref["offsets"][-1])
+    assert plan.send_route_indices.cpu().numpy().tolist() == ref["send_route"].tolist()
+    assert plan.stable_sort_indices.cpu().numpy().tolist() == ref["stable_sort_indices"].tolist()
+    assert plan.received_expert_offsets.cpu().numpy().tolist() == ref["offsets"].tolist()
+    res = op.dispatch_fc1(inp["x"], sel, plan, inp["gate_up"], routing_weights=inp["rw"])
+    torch.cuda.synchronize()
+    st = torch.from_numpy(ref["send_token"]).long()
+    assert torch.equal(res.dispatched_tokens.cpu(), inp["x"].cpu()[st])
+    xp = inp["x"].float().cpu()[st]
+    w1 = inp["gate_up"].float().cpu()
+    o = ref["offsets"]
+    gu = torch.cat([xp[o[e]:o[e + 1]] @ w1[e] for e in range(spec.experts)])
+    assert_rel(res.fc1_output, gu, 1e-2, "fc1_output")
+
+
+def test_autograd_function_matches_backward():
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=11, weight_scale=0.1)
+    op = _op(spec)
+    x = inp["x"].clone().requires_grad_(True)
+    rw = inp["rw"].clone().requires_grad_(True)
+    w1 = inp["gate_up"].clone().requires_grad_(True)
+    w2 = inp["down"].contiguous().clone().requires_grad_(True)
+    out = mega_moe.MegaMoEFunction.apply(op, x, rw, inp["selected"], w1, w2, torch.empty(1, device="cuda"), None)
+    out.backward(inp["dy"])
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"].cpu(), w2.detach().cpu(),
+                            inp["rw"].cpu())
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out.detach(), ref_out, 2e-2, "out")
+    assert_rel(x.grad, ref["grad_hidden"], 2e-2, "dx")
+    assert_rel(rw.grad, ref["grad_routing_weights"], 2e-2, "drw")
+    assert_rel(w1.grad, ref["grad_gate_up"], 2e-2, "dw1")
+    assert_rel(w2.grad, ref["grad_fc2"], 2e-2, "dw2")
+    # a second forward supersedes the first plan: its backward must be rejected
+    out2 = mega_moe.MegaMoEFunction.apply(op, x, rw, inp["selected"], w1, w2, torch.empty(1, device="cuda"), None)
+    out3 = mega_moe.MegaMoEFunction.apply(op, x, rw, inp["selected"], w1, w2, torch.empty(1, device="cuda"), None)
+    with pytest.raises(RuntimeError, match="superseded"):
+        out2.sum().backward()
+    del out3
+
+
+@pytest.mark.parametrize("name", ["e32", "qwen", "skew", "kimi"])
+def test_full_size_sampled_parity(name):
+    """BASELINE sizes: routing bit-exact and sampled output rows vs the oracle."""
+    spec = CASES[name]
+    inp = make_inputs(spec, device="cuda", seed=1234)
+    op = _op(spec)
+    out = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
+    tables = op._route(inp["selected"], inp["rw"])
+    torch.cuda.synchronize()
+    ref = O.route(inp["selected"].cpu().numpy(), spec.experts, spec.top_k)
+    nv = int(ref["offsets"][-1])
+    assert tables.send_route[:nv].cpu().numpy().tolist() == ref["send_route"].tolist()
+    assert tables.route_to_send.cpu().numpy().tolist() == ref["route_to_send"].tolist()
+    toks = [0, 1, spec.tokens // 2, spec.tokens - 1]
+    sub = O.forward_tokens(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"], inp["down"], inp["rw"].cpu(),
+                           toks)
+    assert_rel(out[toks], sub, 2e-2, f"{name} sampled rows")
+    del inp, out
+    torch.cuda.empty_cache()
