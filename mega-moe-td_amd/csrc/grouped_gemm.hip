@@ -24,13 +24,14 @@
 //  * FC1 epilogue: the B tile interleaves 32-column groups of gate and up so
 //    every lane holds gate(i, j) and up(i, j) of the same (row, column) and
 //    applies the weighted gated activation before a single bf16 store.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int BK = 64;
-constexpr int LDS_K = BK + 8;  // row pitch in bf16 elements (144 bytes)
 constexpr int GROUP_M = 8;
 constexpr int kXcds = 8;
 
@@ -86,87 +87,127 @@ __device__ __forceinline__ void grouped_mn(int l, int num_m, int num_n, int& m, 
   n = r / gs;
 }
 
-// ------------------------------------------------------------------ loaders
-// K-contiguous source: ROWS x BK tile; row r starts at row_ptr(r) (nullptr =
-// zero row) and its BK columns k0 .. k0+BK are contiguous.
+// ------------------------------------------------------------------ LDS tiles
+//
+// Both operand tiles are filled with gfx950 global_load_lds_dwordx4: lane l
+// of a wave copies 16 bytes from its own global address to LDS base + 16*l,
+// so each wave instruction fills one contiguous 1 KiB chunk and no staging
+// registers are needed. Bank conflicts of the MFMA fragment reads are removed
+// with XOR swizzles of the 16-byte vector slots, applied on the global side
+// (which source vector a lane fetches) and undone on the LDS read side.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void gbl_void;
+
+constexpr int kChunkElems = 512;  // 1 KiB of bf16 per wave instruction
+
+__device__ __forceinline__ void copy16_to_lds(const bf16* src, bf16* lds_chunk) {
+  __builtin_amdgcn_global_load_lds((gbl_void*)(src), (lds_void*)(lds_chunk), 16, 0, 0);
+}
+
+// gfx950 transposing LDS read: within each 16-lane group, lane i receives
+// element (i % 4) of the 8-byte chunk read by lane 4*j + i/4, for j = 0..3.
+__device__ __forceinline__ v4i16 lds_read_tr16(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+}
+
+// K-contiguous operand: LDS [ROWS][64], vector slot s of row r holds source
+// K-vector s ^ (r & 7). Rows outside the tile point at a valid row; their
+// products are never stored.
 template <int ROWS>
-struct KContigLoader {
-  static constexpr int VPR = BK / 8;  // 16-byte vectors per row
-  static constexpr int VPT = ROWS * VPR / kThreads;
-  static_assert(VPT * kThreads == ROWS * VPR, "tile/threads mismatch");
-  const bf16* ptr[VPT];
-  uint4 reg[VPT];
+struct KcTile {
+  static constexpr int ELEMS = ROWS * BK;
+  static constexpr int CHUNKS = ELEMS / kChunkElems;       // 1 KiB chunks per K step
+  static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
+  static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
+  const bf16* ptr[PER_WAVE];
 
   template <class RowPtr>
   __device__ void init(RowPtr row_ptr) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) {
-      const int idx = threadIdx.x + v * kThreads;
-      const int r = idx / VPR, kv = idx % VPR;
-      const bf16* q = row_ptr(r);
-      ptr[v] = q ? q + kv * 8 : nullptr;
+    for (int v = 0; v < PER_WAVE; ++v) {
+      const int c = v * (kThreads / 64) + wave;
+      const int r = c * 8 + (lane >> 3);
+      const int kv = (lane & 7) ^ (r & 7);
+      ptr[v] = row_ptr(r) + kv * 8;
     }
   }
-  __device__ void load(int k0) {
+  __device__ void issue(bf16* lds, int64_t k0) const {
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < VPT; ++v)
-      reg[v] = ptr[v] ? *reinterpret_cast<const uint4*>(ptr[v] + k0) : make_uint4(0, 0, 0, 0);
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + k0, lds + (v * (kThreads / 64) + wave) * kChunkElems);
   }
-  __device__ void store(bf16* lds) const {
-#pragma unroll
-    for (int v = 0; v < VPT; ++v) {
-      const int idx = threadIdx.x + v * kThreads;
-      const int r = idx / VPR, kv = idx % VPR;
-      *reinterpret_cast<uint4*>(lds + r * LDS_K + kv * 8) = reg[v];
-    }
+  // MFMA 32x32x16 operand: row r0 + lane%32, k = kk + 8*(lane/32) .. +8
+  __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
+    const int r = r0 + (lane & 31);
+    const int kv = (kk >> 3) + (lane >> 5);
+    return *reinterpret_cast<const bf16x8*>(lds + r * BK + ((kv ^ (r & 7)) << 3));
   }
 };
 
-// MN-contiguous source: element (k, c) of the tile lives at k_ptr(k)[col_off(c)]
-// with 8 consecutive tile columns contiguous. Each thread loads 4 consecutive
-// K rows of one 8-column vector and writes them transposed (eight 8-byte LDS
-// stores) into the K-contiguous LDS tile.
-template <int ROWS>
-struct MNContigLoader {
-  static constexpr int NV = ROWS / 8;                   // column vectors
-  static constexpr int QPT = NV * (BK / 4) / kThreads;  // quads per thread
-  static_assert(QPT * kThreads == NV * (BK / 4), "tile/threads mismatch");
-  uint4 reg[QPT][4];
+// Swizzle of the N-contiguous tile: vector slot of (k, source vector cv) is
+// cv ^ mn_swz(k). The pattern keeps the 4 K-rows x 32 bytes touched by a
+// 16-lane transposing read in distinct banks for 128- and 256-byte passes.
+__device__ __forceinline__ int mn_swz(int k) { return (0xEA40 >> ((k & 3) * 4)) & 0xF; }  // {0,4,10,14}
 
-  template <class KPtr, class ColOff>
-  __device__ void load(KPtr k_ptr, ColOff col_off) {
-#pragma unroll
-    for (int q = 0; q < QPT; ++q) {
-      const int idx = threadIdx.x + q * kThreads;
-      const int nv = idx % NV, kq = idx / NV;
-      const int64_t co = col_off(nv * 8);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bf16* src = k_ptr(kq * 4 + i);
-        reg[q][i] = src ? *reinterpret_cast<const uint4*>(src + co) : make_uint4(0, 0, 0, 0);
-      }
-    }
+// M/N-contiguous operand: LDS [64][ROWS] in the source's natural layout
+// (swizzled); MFMA fragments are read with the transposing LDS read.
+template <int ROWS>
+struct MnTile {
+  static constexpr int ELEMS = BK * ROWS;
+  static constexpr int VPR = ROWS / 8;                      // 16-byte vectors per K row
+  static constexpr int CHUNKS = ELEMS / kChunkElems;
+  static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
+  static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
+  static_assert(VPR >= 16, "swizzle needs >= 16 vectors per row");
+  const bf16* ptr[PER_WAVE];
+
+  // K row and source column (elements) this lane copies in instruction v.
+  __device__ static int k_of(int v) {
+    return ((v * (kThreads / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)) / VPR;
   }
-  __device__ void store(bf16* lds) const {
+  __device__ static int col_of(int v) {
+    const int q = (v * (kThreads / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    return ((q % VPR) ^ mn_swz(q / VPR)) * 8;
+  }
+  // Fixed-stride source: element (k, c) at base + k*ld + col_off(c).
+  template <class ColOff>
+  __device__ void init_strided(const bf16* base, int64_t ld, ColOff col_off) {
 #pragma unroll
-    for (int q = 0; q < QPT; ++q) {
-      const int idx = threadIdx.x + q * kThreads;
-      const int nv = idx % NV, kq = idx / NV;
-      const uint32_t w0[4] = {reg[q][0].x, reg[q][0].y, reg[q][0].z, reg[q][0].w};
-      const uint32_t w1[4] = {reg[q][1].x, reg[q][1].y, reg[q][1].z, reg[q][1].w};
-      const uint32_t w2[4] = {reg[q][2].x, reg[q][2].y, reg[q][2].z, reg[q][2].w};
-      const uint32_t w3[4] = {reg[q][3].x, reg[q][3].y, reg[q][3].z, reg[q][3].w};
+    for (int v = 0; v < PER_WAVE; ++v) ptr[v] = base + static_cast<int64_t>(k_of(v)) * ld + col_off(col_of(v));
+  }
+  __device__ void issue(bf16* lds, int64_t off) const {
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int sh = (j & 1) * 16;
-        const uint32_t e0 = (w0[j >> 1] >> sh) & 0xffffu;
-        const uint32_t e1 = (w1[j >> 1] >> sh) & 0xffffu;
-        const uint32_t e2 = (w2[j >> 1] >> sh) & 0xffffu;
-        const uint32_t e3 = (w3[j >> 1] >> sh) & 0xffffu;
-        *reinterpret_cast<uint2*>(lds + (nv * 8 + j) * LDS_K + kq * 4) =
-            make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
-      }
-    }
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + off, lds + (v * (kThreads / 64) + wave) * kChunkElems);
+  }
+  // Per-vector source (wgrad): src(v) -> row pointer (column 0 of the tile)
+  // for the K row this lane copies in instruction v.
+  template <class Src>
+  __device__ static void issue_rows(bf16* lds, Src src) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int v = 0; v < PER_WAVE; ++v)
+      copy16_to_lds(src(v) + col_of(v), lds + (v * (kThreads / 64) + wave) * kChunkElems);
+  }
+  __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
+    const int s = lane & 15, g = lane >> 4;
+    const int k = kk + 8 * (g >> 1) + (s >> 2);
+    const int col = r0 + 16 * (g & 1) + 4 * (s & 3);
+    const bf16* q0 = lds + k * ROWS + ((((col >> 3) ^ mn_swz(k)) << 3) | (col & 7));
+    const bf16* q1 = lds + (k + 4) * ROWS + ((((col >> 3) ^ mn_swz(k + 4)) << 3) | (col & 7));
+    const v4i16 lo = lds_read_tr16(q0);
+    const v4i16 hi = lds_read_tr16(q1);
+    const v8i16 w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, w);
+  }
+  // Zero K rows [k_valid, BK) of a filled tile (ragged K tail).
+  __device__ static void zero_tail(bf16* lds, int k_valid) {
+    for (int i = threadIdx.x; i < (BK - k_valid) * VPR; i += kThreads)
+      reinterpret_cast<uint4*>(lds + k_valid * ROWS)[i] = make_uint4(0, 0, 0, 0);
   }
 };
 
@@ -187,22 +228,29 @@ struct MmaTile {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
+  // One BK-deep step; fragments of sub-step kk+16 are read while the MFMAs of
+  // sub-step kk issue.
+  template <class ATile, class BTile>
   __device__ void compute(const bf16* As, const bf16* Bs, int wm, int wn, int lane) {
-    const int lr = lane & 31, lk = (lane >> 5) * 8;
+    bf16x8 a[2][MI], b[2][NI];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      bf16x8 a[MI], b[NI];
+    for (int i = 0; i < MI; ++i) a[0][i] = ATile::frag(As, wm * TM + i * 32, 0, lane);
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(As + (wm * TM + i * 32 + lr) * LDS_K + kk + lk);
+    for (int j = 0; j < NI; ++j) b[0][j] = BTile::frag(Bs, wn * TN + j * 32, 0, lane);
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(Bs + (wn * TN + j * 32 + lr) * LDS_K + kk + lk);
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) a[nxt][i] = ATile::frag(As, wm * TM + i * 32, (s + 1) * 16, lane);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) b[nxt][j] = BTile::frag(Bs, wn * TN + j * 32, (s + 1) * 16, lane);
+      }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
     }
   }
 
@@ -210,6 +258,38 @@ struct MmaTile {
   // the column is lane & 31.
   __device__ static int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 };
+
+// Epilogue staging: a BM x NC bf16 tile is written to LDS ([BM][NC+8], the
+// padding keeps the two half-waves of a store on different banks), then
+// copied out row by row with 16-byte global stores; rows >= rows are skipped.
+template <int BM, int NC>
+struct StageOut {
+  static constexpr int PITCH = NC + 8;
+  static constexpr int ELEMS = BM * PITCH;
+  __device__ static void put(bf16* lds, int r, int c, float v) {
+    reinterpret_cast<uint16_t*>(lds)[r * PITCH + c] = f32_to_bf16_bits(v);
+  }
+  __device__ static void put_bits(bf16* lds, int r, int c, uint16_t v) {
+    reinterpret_cast<uint16_t*>(lds)[r * PITCH + c] = v;
+  }
+  // out points at (row 0, column 0) of the tile; ld in elements.
+  __device__ static void flush(const bf16* lds, int rows, bf16* out, int64_t ld) {
+    __syncthreads();
+    constexpr int VPR = NC / 8;
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+      const int r = idx / VPR, cv = idx % VPR;
+      if (r < rows)
+        *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * ld + cv * 8) =
+            *reinterpret_cast<const uint4*>(lds + r * PITCH + cv * 8);
+    }
+    __syncthreads();
+  }
+};
+
+__device__ __forceinline__ void wait_loads_and_sync() {
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt/lgkmcnt = 0: this wave's LDS copies landed
+  __syncthreads();
+}
 
 // ------------------------------------------------------------------ row GEMM
 struct RowsArgs {
@@ -236,8 +316,13 @@ enum { B_KCONTIG = 0, B_NCONTIG = 1 };
 template <int BM, int BN, int WM, int WN, int BLAYOUT, int EPI>
 __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
   using Mma = MmaTile<BM, BN, WM, WN>;
-  static_assert(EPI != EPI_GATED || (Mma::NI == 2 && BLAYOUT == B_NCONTIG), "gated epilogue layout");
-  __shared__ __attribute__((aligned(16))) bf16 smem[2][(BM + BN) * LDS_K];
+  using ATile = KcTile<BM>;
+  using BTile = typename std::conditional<BLAYOUT == B_KCONTIG, KcTile<BN>, MnTile<BN>>::type;
+  static_assert(EPI != EPI_GATED || (Mma::NI % 2 == 0 && BLAYOUT == B_NCONTIG), "gated epilogue layout");
+  constexpr int STAGE = ATile::ELEMS + BTile::ELEMS;
+  using Out = StageOut<BM, BN>;
+  constexpr int SMEM = (2 * STAGE > Out::ELEMS) ? 2 * STAGE : Out::ELEMS;
+  __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
 
   const int num_m = p.tl->count;
   const int num_n = p.n / BN;
@@ -252,62 +337,52 @@ __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
   const int n0 = nt * BN;
   const bf16* bexp = p.b + static_cast<int64_t>(e) * p.b_se;
 
-  KContigLoader<BM> la;
+  ATile la;
   la.init([&](int r) -> const bf16* {
-    if (r >= rows) return nullptr;
-    const int64_t src = p.a_rows ? static_cast<int64_t>(p.a_rows[row0 + r]) : static_cast<int64_t>(row0 + r);
+    const int rr = row0 + min(r, rows - 1);  // rows past the tile re-read its last row
+    const int64_t src = p.a_rows ? static_cast<int64_t>(p.a_rows[rr]) : static_cast<int64_t>(rr);
     return p.a + src * p.lda;
   });
 
-  // B tile column c -> global column n (gated: 32-wide gate/up interleave).
+  // B tile column c -> global column n. Gated: each wave's TN columns hold
+  // 32-wide groups alternating gate / up of the same output columns.
   auto bcol = [&](int c) -> int64_t {
     if constexpr (EPI == EPI_GATED) {
-      const int wnc = c / 64, sub = (c / 32) & 1, jj = c & 31;
-      return static_cast<int64_t>(sub) * p.inter + nt * (BN / 2) + wnc * 32 + jj;
+      const int wnc = c / Mma::TN, ni = (c % Mma::TN) / 32, jj = c & 31;
+      return static_cast<int64_t>(ni & 1) * p.inter + nt * (BN / 2) + wnc * (Mma::TN / 2) + (ni >> 1) * 32 + jj;
     } else {
       return n0 + c;
     }
   };
 
-  KContigLoader<BN> lbk;
-  MNContigLoader<BN> lbn;
+  BTile lb;
+  int64_t b_step;  // element offset of one BK step along K
   if constexpr (BLAYOUT == B_KCONTIG) {
-    lbk.init([&](int c) -> const bf16* { return bexp + bcol(c) * p.b_sn; });
+    lb.init([&](int c) -> const bf16* { return bexp + bcol(c) * p.b_sn; });
+    b_step = BK;
+  } else {
+    lb.init_strided(bexp, p.b_sk, bcol);
+    b_step = static_cast<int64_t>(BK) * p.b_sk;
   }
-  auto load_b = [&](int k0) {
-    if constexpr (BLAYOUT == B_KCONTIG) {
-      lbk.load(k0);
-    } else {
-      lbn.load([&](int kk) -> const bf16* { return bexp + static_cast<int64_t>(k0 + kk) * p.b_sk; }, bcol);
-    }
-  };
-  auto store_b = [&](bf16* lds) {
-    if constexpr (BLAYOUT == B_KCONTIG) lbk.store(lds); else lbn.store(lds);
-  };
 
   Mma mma;
   mma.zero();
   const int nk = p.k / BK;
-  la.load(0);
-  load_b(0);
-  la.store(smem[0]);
-  store_b(smem[0] + BM * LDS_K);
-  __syncthreads();
+  la.issue(smem, 0);
+  lb.issue(smem + ATile::ELEMS, 0);
+  wait_loads_and_sync();
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+    bf16* cur = smem + (kt & 1) * STAGE;
+    bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
     if (kt + 1 < nk) {
-      la.load((kt + 1) * BK);
-      load_b((kt + 1) * BK);
+      la.issue(nxt, static_cast<int64_t>(kt + 1) * BK);
+      lb.issue(nxt + ATile::ELEMS, (kt + 1) * b_step);
     }
-    mma.compute(smem[cur], smem[cur] + BM * LDS_K, wm, wn, lane);
-    if (kt + 1 < nk) {
-      la.store(smem[cur ^ 1]);
-      store_b(smem[cur ^ 1] + BM * LDS_K);
-    }
-    __syncthreads();
+    mma.template compute<ATile, BTile>(cur, cur + ATile::ELEMS, wm, wn, lane);
+    wait_loads_and_sync();
   }
 
-  // ---- epilogue
+  // ---- epilogue (LDS-staged, 16-byte stores)
   const int col = lane & 31;
   if constexpr (EPI == EPI_STORE) {
 #pragma unroll
@@ -315,35 +390,50 @@ __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
 #pragma unroll
       for (int j = 0; j < Mma::NI; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tr = wm * Mma::TM + i * 32 + Mma::acc_row(r, lane);
-          if (tr < rows) {
-            const int tc = wn * Mma::TN + j * 32 + col;
-            reinterpret_cast<uint16_t*>(p.c)[static_cast<int64_t>(row0 + tr) * p.ldc + n0 + tc] =
-                f32_to_bf16_bits(mma.acc[i][j][r]);
-          }
-        }
+        for (int r = 0; r < 16; ++r)
+          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + j * 32 + col,
+                   mma.acc[i][j][r]);
+    Out::flush(smem, rows, p.c + static_cast<int64_t>(row0) * p.ldc + n0, p.ldc);
   } else {
-    const int jcol = nt * (BN / 2) + wn * 32 + col;  // gate/up column index in [0, I)
+    // Stage bf16(gate) in LDS columns [0, BN/2) and bf16(up) in [BN/2, BN)
+    // (tile column = output column - jbase), then each thread turns one
+    // 8-column vector of a row into act = bf16(act_fn(gate, up) * w[row]).
+    const int jbase = nt * (BN / 2);
 #pragma unroll
     for (int i = 0; i < Mma::MI; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tr = wm * Mma::TM + i * 32 + Mma::acc_row(r, lane);
-        if (tr < rows) {
-          const int64_t row = row0 + tr;
-          const uint16_t gb = f32_to_bf16_bits(mma.acc[i][0][r]);
-          const uint16_t ub = f32_to_bf16_bits(mma.acc[i][1][r]);
-          if (p.fc1_out) {
-            uint16_t* fo = reinterpret_cast<uint16_t*>(p.fc1_out) + row * (2 * static_cast<int64_t>(p.inter));
-            fo[jcol] = gb;
-            fo[p.inter + jcol] = ub;
-          }
-          const float v = gated_act(p.act_kind, bf16_bits_to_f32(gb), bf16_bits_to_f32(ub), p.beta, p.lbeta,
-                                    p.clamp) * p.w[row];
-          reinterpret_cast<uint16_t*>(p.c)[row * p.ldc + jcol] = f32_to_bf16_bits(v);
-        }
+      for (int jj = 0; jj < Mma::NI; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane),
+                   (jj & 1) * (BN / 2) + wn * (Mma::TN / 2) + (jj >> 1) * 32 + col, mma.acc[i][jj][r]);
+    __syncthreads();
+    constexpr int VPR = BN / 16;  // 8-column vectors per output row
+    const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+      const int r = idx / VPR, cv = idx % VPR;
+      if (r >= rows) continue;
+      const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
+      const uint4 uv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + BN / 2 + cv * 8);
+      const int64_t row = row0 + r;
+      const float wr = p.w[row];
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a0 = gated_act(p.act_kind, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
+                                   p.beta, p.lbeta, p.clamp) * wr;
+        const float a1 = gated_act(p.act_kind, __uint_as_float(gw[q] & 0xffff0000u),
+                                   __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
+        ow[q] = static_cast<uint32_t>(f32_to_bf16_bits(a0)) | (static_cast<uint32_t>(f32_to_bf16_bits(a1)) << 16);
       }
+      *reinterpret_cast<uint4*>(p.c + row * p.ldc + jbase + cv * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      if (p.fc1_out) {
+        bf16* fo = p.fc1_out + row * ldf + jbase + cv * 8;
+        *reinterpret_cast<uint4*>(fo) = gv;
+        *reinterpret_cast<uint4*>(fo + p.inter) = uv;
+      }
+    }
   }
 }
 
@@ -360,95 +450,148 @@ struct WgradArgs {
   bf16* c;
 };
 
+// Scheduling: the (t1, t2) tiles of every expert are split into 8 equal
+// slices and slice x runs on XCD x (workgroup ids congruent to x mod 8), so
+// hot and cold experts are spread evenly over the XCDs whatever the routing
+// skew, while each XCD still sweeps a contiguous, L2-friendly block of one
+// expert's tiles.
 template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, int num_experts) {
+__global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, int num_experts, int per_xcd) {
   using Mma = MmaTile<BM, BN, WM, WN>;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2][(BM + BN) * LDS_K];
+  using PTile = MnTile<BM>;
+  using QTile = MnTile<BN>;
+  constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
+  using Out = StageOut<BM, BN>;
+  constexpr int SMEM = (2 * STAGE > Out::ELEMS) ? 2 * STAGE : Out::ELEMS;
+  __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
   const int t1n = a.n1 / BM, t2n = a.n2 / BN;
   const int per_e = t1n * t2n;
-  const int l = xcd_remap(blockIdx.x, num_experts * per_e);
-  if (l < 0) return;
-  const int e = l / per_e;
+  const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int e = j / per_xcd;
+  const int t = x * per_xcd + (j - e * per_xcd);
+  if (e >= num_experts || t >= per_e) return;
   int t1, t2;
-  grouped_mn(l - e * per_e, t1n, t2n, t1, t2);
+  grouped_mn(t, t1n, t2n, t1, t2);
   const int r0 = a.offsets[e], r1 = a.offsets[e + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  MNContigLoader<BM> lp;
-  MNContigLoader<BN> lq;
-  auto load = [&](int k0) {
-    lp.load(
-        [&](int kk) -> const bf16* {
-          const int r = r0 + k0 + kk;
-          if (r >= r1) return nullptr;
-          const int64_t src = a.p_rows ? static_cast<int64_t>(a.p_rows[r]) : static_cast<int64_t>(r);
-          return a.p + src * a.ldp;
-        },
-        [&](int c) -> int64_t { return static_cast<int64_t>(t1) * BM + c; });
-    lq.load(
-        [&](int kk) -> const bf16* {
-          const int r = r0 + k0 + kk;
-          if (r >= r1) return nullptr;
-          const int64_t src = a.q_rows ? static_cast<int64_t>(a.q_rows[r]) : static_cast<int64_t>(r);
-          return a.q + src * a.ldq;
-        },
-        [&](int c) -> int64_t { return static_cast<int64_t>(t2) * BN + c; });
+  // Source rows of the next K step are resolved one step ahead so the index
+  // loads never stall the copies.
+  int prow[PTile::PER_WAVE], qrow[QTile::PER_WAVE];
+  auto fetch_rows = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < PTile::PER_WAVE; ++v) {
+      const int r = min(r0 + k0 + PTile::k_of(v), r1 - 1);
+      prow[v] = a.p_rows ? a.p_rows[r] : r;
+    }
+#pragma unroll
+    for (int v = 0; v < QTile::PER_WAVE; ++v) {
+      const int r = min(r0 + k0 + QTile::k_of(v), r1 - 1);
+      qrow[v] = a.q_rows ? a.q_rows[r] : r;
+    }
+  };
+  const int64_t pc = static_cast<int64_t>(t1) * BM, qc = static_cast<int64_t>(t2) * BN;
+  auto issue = [&](bf16* buf) {
+    PTile::issue_rows(buf, [&](int v) { return a.p + static_cast<int64_t>(prow[v]) * a.ldp + pc; });
+    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) { return a.q + static_cast<int64_t>(qrow[v]) * a.ldq + qc; });
+  };
+  // After a step's copies landed: zero the K rows past the expert's end.
+  auto fix_tail = [&](bf16* buf, int k0) {
+    const int kv = r1 - r0 - k0;
+    if (kv < BK) {
+      __syncthreads();
+      PTile::zero_tail(buf, kv);
+      QTile::zero_tail(buf + PTile::ELEMS, kv);
+      __syncthreads();
+    }
   };
 
   Mma mma;
   mma.zero();
   const int nk = (r1 - r0 + BK - 1) / BK;
   if (nk > 0) {
-    load(0);
-    lp.store(smem[0]);
-    lq.store(smem[0] + BM * LDS_K);
-    __syncthreads();
+    fetch_rows(0);
+    issue(smem);
+    if (nk > 1) fetch_rows(BK);
+    wait_loads_and_sync();
+    fix_tail(smem, 0);
     for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load((kt + 1) * BK);
-      mma.compute(smem[cur], smem[cur] + BM * LDS_K, wm, wn, lane);
+      bf16* cur = smem + (kt & 1) * STAGE;
+      bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
       if (kt + 1 < nk) {
-        lp.store(smem[cur ^ 1]);
-        lq.store(smem[cur ^ 1] + BM * LDS_K);
+        issue(nxt);
+        if (kt + 2 < nk) fetch_rows((kt + 2) * BK);
       }
-      __syncthreads();
+      mma.template compute<PTile, QTile>(cur, cur + PTile::ELEMS, wm, wn, lane);
+      wait_loads_and_sync();
+      if (kt + 1 < nk) fix_tail(nxt, (kt + 1) * BK);
     }
   }
-  uint16_t* out = reinterpret_cast<uint16_t*>(a.c) + static_cast<int64_t>(e) * a.n1 * a.n2;
   const int col = lane & 31;
+  if (nk == 0) __syncthreads();
 #pragma unroll
   for (int i = 0; i < Mma::MI; ++i)
 #pragma unroll
-    for (int j = 0; j < Mma::NI; ++j)
+    for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = static_cast<int64_t>(t1) * BM + wm * Mma::TM + i * 32 + Mma::acc_row(r, lane);
-        const int64_t cc = static_cast<int64_t>(t2) * BN + wn * Mma::TN + j * 32 + col;
-        out[row * a.n2 + cc] = f32_to_bf16_bits(mma.acc[i][j][r]);
-      }
+      for (int r = 0; r < 16; ++r)
+        Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + jj * 32 + col,
+                 mma.acc[i][jj][r]);
+  Out::flush(smem, BM, a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + static_cast<int64_t>(t1) * BM * a.n2 + t2 * BN,
+             a.n2);
 }
 
 // ------------------------------------------------------------------ host side
-constexpr int kBM = 128, kBN = 128, kWM = 2, kWN = 2;
+constexpr int kMinBM = 128;  // smallest M tile: sizes the tile list
 
 int64_t max_m_tiles(int64_t max_rows, int E, int BM) { return (max_rows + BM - 1) / BM + E; }
 
 size_t tile_list_bytes(int64_t max_rows, int E) {
-  return mm_align_up(sizeof(TileList) + sizeof(int4) * static_cast<size_t>(max_m_tiles(max_rows, E, kBM)), 256);
+  return mm_align_up(sizeof(TileList) + sizeof(int4) * static_cast<size_t>(max_m_tiles(max_rows, E, kMinBM)), 256);
 }
 
-int launch_tiles(const int32_t* offsets, int E, void* ws, hipStream_t s) {
-  build_tiles_kernel<<<1, 1024, 0, s>>>(offsets, E, kBM, static_cast<TileList*>(ws));
+int launch_tiles(const int32_t* offsets, int E, int BM, void* ws, hipStream_t s) {
+  build_tiles_kernel<<<1, 1024, 0, s>>>(offsets, E, BM, static_cast<TileList*>(ws));
   return mm_check_launch("build_tiles");
 }
 
-int rows_grid(int64_t max_rows, int E, int n, int BN) {
-  const int64_t g = max_m_tiles(max_rows, E, kBM) * (n / BN);
-  return static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Row-GEMM tile choice: 256x256 when experts average >= 256 rows, else a
+// 128-row tile; 256-wide N tiles when N allows.
+struct RowsCfg {
+  int bm, bn;
+};
+
+RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
+  RowsCfg c;
+  c.bn = (n % 256 == 0) ? 256 : 128;
+  c.bm = (c.bn == 256 && max_rows / E >= 256) ? 256 : 128;
+  return c;
 }
 
-bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+template <int BM, int BN, int BLAYOUT, int EPI>
+void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
+  const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
+  const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
+  grouped_rows_kernel<BM, BN, 2, 2, BLAYOUT, EPI><<<grid, kThreads, 0, s>>>(p);
+}
+
+template <int BLAYOUT, int EPI>
+int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* ws, hipStream_t s,
+             const char* what) {
+  const RowsCfg c = pick_rows_cfg(max_rows, E, p.n);
+  if (int rc = launch_tiles(offsets, E, c.bm, ws, s)) return rc;
+  p.tl = static_cast<const TileList*>(ws);
+  if (c.bm == 256)
+    launch_rows_cfg<256, 256, BLAYOUT, EPI>(p, max_rows, E, s);
+  else if (c.bn == 256)
+    launch_rows_cfg<128, 256, BLAYOUT, EPI>(p, max_rows, E, s);
+  else
+    launch_rows_cfg<128, 128, BLAYOUT, EPI>(p, max_rows, E, s);
+  return mm_check_launch(what);
+}
 
 }  // namespace
 
@@ -464,7 +607,7 @@ extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send
   MM_CHECK_ARG(x && w1 && offsets && weight_perm && act, "mm_fc1_swiglu: null pointer");
   MM_CHECK_ARG(num_experts > 0 && max_rows >= 0 && max_rows < (int64_t(1) << 31), "mm_fc1_swiglu: bad sizes");
   MM_CHECK_ARG(hidden > 0 && hidden % BK == 0, "mm_fc1_swiglu: hidden must be a multiple of %d", BK);
-  MM_CHECK_ARG(inter > 0 && inter % (kBN / 2) == 0, "mm_fc1_swiglu: inter must be a multiple of %d", kBN / 2);
+  MM_CHECK_ARG(inter > 0 && inter % 64 == 0, "mm_fc1_swiglu: inter must be a multiple of 64");
   MM_CHECK_ARG(ldx % 8 == 0 && al16(x) && al16(w1), "mm_fc1_swiglu: 16-byte alignment required");
   MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_fc1_swiglu: bad act_kind");
   if (!workspace || workspace_bytes < tile_list_bytes(max_rows, num_experts)) {
@@ -472,8 +615,6 @@ extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send
     return MM_E_WS;
   }
   if (max_rows == 0) return MM_OK;
-  hipStream_t s = mm_hip_stream(stream);
-  if (int rc = launch_tiles(offsets, num_experts, workspace, s)) return rc;
   RowsArgs p{};
   p.a = reinterpret_cast<const bf16*>(x);
   p.lda = ldx;
@@ -486,7 +627,6 @@ extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send
   p.k = hidden;
   p.c = reinterpret_cast<bf16*>(act);
   p.ldc = inter;
-  p.tl = static_cast<const TileList*>(workspace);
   p.w = weight_perm;
   p.fc1_out = reinterpret_cast<bf16*>(fc1_out);
   p.inter = inter;
@@ -494,9 +634,8 @@ extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send
   p.beta = situ_beta;
   p.lbeta = situ_linear_beta;
   p.clamp = clamp_limit;
-  grouped_rows_kernel<kBM, kBN, kWM, kWN, B_NCONTIG, EPI_GATED>
-      <<<rows_grid(max_rows, num_experts, p.n, kBN), kThreads, 0, s>>>(p);
-  return mm_check_launch("mm_fc1_swiglu");
+  return run_rows<B_NCONTIG, EPI_GATED>(p, offsets, max_rows, num_experts, workspace, mm_hip_stream(stream),
+                                        "mm_fc1_swiglu");
 }
 
 extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b,
@@ -505,7 +644,7 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
                                int64_t ldc, void* workspace, size_t workspace_bytes, mm_stream_t stream) {
   MM_CHECK_ARG(a && b && offsets && c, "mm_grouped_gemm: null pointer");
   MM_CHECK_ARG(num_experts > 0 && max_rows >= 0 && max_rows < (int64_t(1) << 31), "mm_grouped_gemm: bad sizes");
-  MM_CHECK_ARG(n > 0 && n % kBN == 0, "mm_grouped_gemm: n must be a multiple of %d", kBN);
+  MM_CHECK_ARG(n > 0 && n % 128 == 0, "mm_grouped_gemm: n must be a multiple of 128");
   MM_CHECK_ARG(k > 0 && k % BK == 0, "mm_grouped_gemm: k must be a multiple of %d", BK);
   MM_CHECK_ARG(b_sn == 1 || b_sk == 1, "mm_grouped_gemm: B must be contiguous along N or K");
   MM_CHECK_ARG(lda % 8 == 0 && al16(a) && al16(b) && (b_sn == 1 ? b_sk % 8 == 0 : b_sn % 8 == 0) &&
@@ -516,8 +655,6 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
     return MM_E_WS;
   }
   if (max_rows == 0) return MM_OK;
-  hipStream_t s = mm_hip_stream(stream);
-  if (int rc = launch_tiles(offsets, num_experts, workspace, s)) return rc;
   RowsArgs p{};
   p.a = reinterpret_cast<const bf16*>(a);
   p.lda = lda;
@@ -530,13 +667,9 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
   p.k = k;
   p.c = reinterpret_cast<bf16*>(c);
   p.ldc = ldc;
-  p.tl = static_cast<const TileList*>(workspace);
-  const int grid = rows_grid(max_rows, num_experts, n, kBN);
-  if (b_sk == 1)
-    grouped_rows_kernel<kBM, kBN, kWM, kWN, B_KCONTIG, EPI_STORE><<<grid, kThreads, 0, s>>>(p);
-  else
-    grouped_rows_kernel<kBM, kBN, kWM, kWN, B_NCONTIG, EPI_STORE><<<grid, kThreads, 0, s>>>(p);
-  return mm_check_launch("mm_grouped_gemm");
+  hipStream_t s = mm_hip_stream(stream);
+  if (b_sk == 1) return run_rows<B_KCONTIG, EPI_STORE>(p, offsets, max_rows, num_experts, workspace, s, "mm_grouped_gemm");
+  return run_rows<B_NCONTIG, EPI_STORE>(p, offsets, max_rows, num_experts, workspace, s, "mm_grouped_gemm");
 }
 
 extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows, const uint16_t* q,
@@ -547,14 +680,26 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   (void)workspace_bytes;
   MM_CHECK_ARG(p && q && offsets && c, "mm_grouped_wgrad: null pointer");
   MM_CHECK_ARG(num_experts > 0, "mm_grouped_wgrad: bad num_experts");
-  MM_CHECK_ARG(n1 > 0 && n1 % kBM == 0 && n2 > 0 && n2 % kBN == 0,
-               "mm_grouped_wgrad: n1, n2 must be multiples of %d", kBM);
+  MM_CHECK_ARG(n1 > 0 && n1 % 128 == 0 && n2 > 0 && n2 % 128 == 0, "mm_grouped_wgrad: n1, n2 must be multiples of 128");
   MM_CHECK_ARG(ldp % 8 == 0 && ldq % 8 == 0 && al16(p) && al16(q), "mm_grouped_wgrad: 16-byte alignment required");
-  WgradArgs a{p ? reinterpret_cast<const bf16*>(p) : nullptr, ldp, p_rows, reinterpret_cast<const bf16*>(q), ldq,
+  WgradArgs a{reinterpret_cast<const bf16*>(p), ldp, p_rows, reinterpret_cast<const bf16*>(q), ldq,
               q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c)};
-  const int64_t tiles = static_cast<int64_t>(num_experts) * (n1 / kBM) * (n2 / kBN);
-  MM_CHECK_ARG(tiles < (int64_t(1) << 31) - 8, "mm_grouped_wgrad: too many tiles");
-  const int grid = static_cast<int>((tiles + kXcds - 1) / kXcds * kXcds);
-  grouped_wgrad_kernel<kBM, kBN, kWM, kWN><<<grid, kThreads, 0, mm_hip_stream(stream)>>>(a, num_experts);
+  const int bm = (n1 % 256 == 0) ? 256 : 128;
+  const int bn = (n2 % 256 == 0) ? 256 : 128;
+  const int64_t per_e = static_cast<int64_t>(n1 / bm) * (n2 / bn);
+  const int64_t per_xcd = (per_e + kXcds - 1) / kXcds;
+  const int64_t grid64 = static_cast<int64_t>(num_experts) * per_xcd * kXcds;
+  MM_CHECK_ARG(grid64 < (int64_t(1) << 31), "mm_grouped_wgrad: too many tiles");
+  const int grid = static_cast<int>(grid64);
+  const int px = static_cast<int>(per_xcd);
+  hipStream_t s = mm_hip_stream(stream);
+  if (bm == 256 && bn == 256)
+    grouped_wgrad_kernel<256, 256, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  else if (bm == 256)
+    grouped_wgrad_kernel<256, 128, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  else if (bn == 256)
+    grouped_wgrad_kernel<128, 256, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  else
+    grouped_wgrad_kernel<128, 128, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   return mm_check_launch("mm_grouped_wgrad");
 }
