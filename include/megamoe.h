@@ -128,15 +128,17 @@ int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows,
  * Grouped weight-gradient GEMM with ragged K (the expert's rows):
  *   c[e, n1, n2] = sum_{i in rows(e)} p[prow(i), n1] * q[qrow(i), n2]
  * prow(i) = p_rows[i] if p_rows != NULL else i (same for q). Output bf16
- * [E, N1, N2] contiguous; experts with no rows get zeros.
+ * [E, N1, N2] contiguous; experts with no rows get zeros. max_rows is the
+ * row capacity (an upper bound of offsets[E]); it only selects the tiling.
  * Replaces kernels/transposed_grouped_gemm.py:24-100 and the default
  * torch_npu grouped wgrad of ops/backward.py:85-94.
  */
 int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows,
                      const uint16_t* q, int64_t ldq, const int32_t* q_rows,
-                     const int32_t* offsets, int32_t num_experts, int32_t n1,
-                     int32_t n2, uint16_t* c, void* workspace,
-                     size_t workspace_bytes, mm_stream_t stream);
+                     const int32_t* offsets, int32_t num_experts,
+                     int64_t max_rows, int32_t n1, int32_t n2, uint16_t* c,
+                     void* workspace, size_t workspace_bytes,
+                     mm_stream_t stream);
 
 /* ---------------------------------------------------------------- combine */
 

@@ -24,6 +24,9 @@
 //  * FC1 epilogue: the B tile interleaves 32-column groups of gate and up so
 //    every lane holds gate(i, j) and up(i, j) of the same (row, column) and
 //    applies the weighted gated activation before a single bf16 store.
+#include <stdlib.h>
+#include <string.h>
+
 #include <type_traits>
 
 #include "common.h"
@@ -100,11 +103,34 @@ typedef short v8i16 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void gbl_void;
+typedef __attribute__((address_space(4))) const int32_t const_i32;
 
 constexpr int kChunkElems = 512;  // 1 KiB of bf16 per wave instruction
 
+// LDS-DMA copy issued from inline asm: the compiler does not track it, so it
+// adds no conservative vmcnt(0) before later LDS reads (it would otherwise
+// serialise every prefetch); completion is awaited explicitly with
+// wait_vmcnt<N>() + a barrier. M0 (the LDS destination) is written only here.
 __device__ __forceinline__ void copy16_to_lds(const bf16* src, bf16* lds_chunk) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)(src), (lds_void*)(lds_chunk), 16, 0, 0);
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(lds_chunk))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+}
+
+// s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// wait until at most n * PER vector-memory ops of this wave are in flight
+template <int PER, int MAXN>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (MAXN >= 3) { if (n >= 3) { wait_vmcnt<3 * PER>(); return; } }
+  if constexpr (MAXN >= 2) { if (n == 2) { wait_vmcnt<2 * PER>(); return; } }
+  if constexpr (MAXN >= 1) { if (n == 1) { wait_vmcnt<PER>(); return; } }
+  wait_vmcnt<0>();
 }
 
 // gfx950 transposing LDS read: within each 16-lane group, lane i receives
@@ -113,26 +139,30 @@ __device__ __forceinline__ v4i16 lds_read_tr16(const bf16* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
 }
 
-// K-contiguous operand: LDS [ROWS][64], vector slot s of row r holds source
-// K-vector s ^ (r & 7). Rows outside the tile point at a valid row; their
-// products are never stored.
-template <int ROWS>
+// K-contiguous operand: LDS [ROWS][BK_] (BK_ = 64 or 32). Vector slot s of
+// row r holds source K-vector s ^ swz(r): for 128-byte rows swz = r & 7, for
+// 64-byte rows swz = (r >> 1) & 3, so the 8 rows touched by one pass of a
+// 16-byte fragment read land in distinct banks. Rows outside the tile point
+// at a valid row; their products are never stored.
+template <int ROWS, int BK_>
 struct KcTile {
-  static constexpr int ELEMS = ROWS * BK;
+  static constexpr int ELEMS = ROWS * BK_;
+  static constexpr int VPR = BK_ / 8;                      // vectors per row
   static constexpr int CHUNKS = ELEMS / kChunkElems;       // 1 KiB chunks per K step
   static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
   static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
   const bf16* ptr[PER_WAVE];
+
+  __device__ static int swz(int r) { return VPR == 8 ? (r & 7) : ((r >> 1) & 3); }
 
   template <class RowPtr>
   __device__ void init(RowPtr row_ptr) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v) {
-      const int c = v * (kThreads / 64) + wave;
-      const int r = c * 8 + (lane >> 3);
-      const int kv = (lane & 7) ^ (r & 7);
-      ptr[v] = row_ptr(r) + kv * 8;
+      const int q = (v * (kThreads / 64) + wave) * 64 + lane;
+      const int r = q / VPR;
+      ptr[v] = row_ptr(r) + ((q % VPR) ^ swz(r)) * 8;
     }
   }
   __device__ void issue(bf16* lds, int64_t k0) const {
@@ -144,7 +174,7 @@ struct KcTile {
   __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
     const int r = r0 + (lane & 31);
     const int kv = (kk >> 3) + (lane >> 5);
-    return *reinterpret_cast<const bf16x8*>(lds + r * BK + ((kv ^ (r & 7)) << 3));
+    return *reinterpret_cast<const bf16x8*>(lds + r * BK_ + ((kv ^ swz(r)) << 3));
   }
 };
 
@@ -153,14 +183,15 @@ struct KcTile {
 // 16-lane transposing read in distinct banks for 128- and 256-byte passes.
 __device__ __forceinline__ int mn_swz(int k) { return (0xEA40 >> ((k & 3) * 4)) & 0xF; }  // {0,4,10,14}
 
-// M/N-contiguous operand: LDS [64][ROWS] in the source's natural layout
+// M/N-contiguous operand: LDS [BK_][ROWS] in the source's natural layout
 // (swizzled); MFMA fragments are read with the transposing LDS read.
-template <int ROWS>
+template <int ROWS, int BK_>
 struct MnTile {
-  static constexpr int ELEMS = BK * ROWS;
+  static constexpr int ELEMS = BK_ * ROWS;
   static constexpr int VPR = ROWS / 8;                      // 16-byte vectors per K row
   static constexpr int CHUNKS = ELEMS / kChunkElems;
   static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
+  static constexpr int KPC = 64 / VPR;                      // K rows per 1 KiB chunk
   static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
   static_assert(VPR >= 16, "swizzle needs >= 16 vectors per row");
   const bf16* ptr[PER_WAVE];
@@ -204,9 +235,9 @@ struct MnTile {
     const v8i16 w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_bit_cast(bf16x8, w);
   }
-  // Zero K rows [k_valid, BK) of a filled tile (ragged K tail).
+  // Zero K rows [k_valid, BK_) of a filled tile (ragged K tail).
   __device__ static void zero_tail(bf16* lds, int k_valid) {
-    for (int i = threadIdx.x; i < (BK - k_valid) * VPR; i += kThreads)
+    for (int i = threadIdx.x; i < (BK_ - k_valid) * VPR; i += kThreads)
       reinterpret_cast<uint4*>(lds + k_valid * ROWS)[i] = make_uint4(0, 0, 0, 0);
   }
 };
@@ -228,19 +259,22 @@ struct MmaTile {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
-  // One BK-deep step; fragments of sub-step kk+16 are read while the MFMAs of
-  // sub-step kk issue.
-  template <class ATile, class BTile>
+  // One BK_-deep step; fragments of sub-step kk+16 are read while the MFMAs
+  // of sub-step kk issue.
+  template <class ATile, class BTile, int BK_>
   __device__ void compute(const bf16* As, const bf16* Bs, int wm, int wn, int lane) {
+#ifdef MM_IGLP
+    __builtin_amdgcn_iglp_opt(MM_IGLP);
+#endif
     bf16x8 a[2][MI], b[2][NI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) a[0][i] = ATile::frag(As, wm * TM + i * 32, 0, lane);
 #pragma unroll
     for (int j = 0; j < NI; ++j) b[0][j] = BTile::frag(Bs, wn * TN + j * 32, 0, lane);
 #pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
+    for (int s = 0; s < BK_ / 16; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
-      if (s + 1 < BK / 16) {
+      if (s + 1 < BK_ / 16) {
 #pragma unroll
         for (int i = 0; i < MI; ++i) a[nxt][i] = ATile::frag(As, wm * TM + i * 32, (s + 1) * 16, lane);
 #pragma unroll
@@ -269,9 +303,6 @@ struct StageOut {
   __device__ static void put(bf16* lds, int r, int c, float v) {
     reinterpret_cast<uint16_t*>(lds)[r * PITCH + c] = f32_to_bf16_bits(v);
   }
-  __device__ static void put_bits(bf16* lds, int r, int c, uint16_t v) {
-    reinterpret_cast<uint16_t*>(lds)[r * PITCH + c] = v;
-  }
   // out points at (row 0, column 0) of the tile; ld in elements.
   __device__ static void flush(const bf16* lds, int rows, bf16* out, int64_t ld) {
     __syncthreads();
@@ -282,14 +313,8 @@ struct StageOut {
         *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * ld + cv * 8) =
             *reinterpret_cast<const uint4*>(lds + r * PITCH + cv * 8);
     }
-    __syncthreads();
   }
 };
-
-__device__ __forceinline__ void wait_loads_and_sync() {
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt/lgkmcnt = 0: this wave's LDS copies landed
-  __syncthreads();
-}
 
 // ------------------------------------------------------------------ row GEMM
 struct RowsArgs {
@@ -313,15 +338,19 @@ struct RowsArgs {
 enum { EPI_STORE = 0, EPI_GATED = 1 };
 enum { B_KCONTIG = 0, B_NCONTIG = 1 };
 
-template <int BM, int BN, int WM, int WN, int BLAYOUT, int EPI>
+// NST-stage ring of LDS buffers: stage s is copied into buffer s % NST while
+// the MFMAs consume stage s - NST + 1; one barrier per K step.
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI>
 __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
+  constexpr int WM = 2, WN = 2;
   using Mma = MmaTile<BM, BN, WM, WN>;
-  using ATile = KcTile<BM>;
-  using BTile = typename std::conditional<BLAYOUT == B_KCONTIG, KcTile<BN>, MnTile<BN>>::type;
+  using ATile = KcTile<BM, BK_>;
+  using BTile = typename std::conditional<BLAYOUT == B_KCONTIG, KcTile<BN, BK_>, MnTile<BN, BK_>>::type;
   static_assert(EPI != EPI_GATED || (Mma::NI % 2 == 0 && BLAYOUT == B_NCONTIG), "gated epilogue layout");
   constexpr int STAGE = ATile::ELEMS + BTile::ELEMS;
+  constexpr int LPS = ATile::PER_WAVE + BTile::PER_WAVE;  // copies per wave per stage
   using Out = StageOut<BM, BN>;
-  constexpr int SMEM = (2 * STAGE > Out::ELEMS) ? 2 * STAGE : Out::ELEMS;
+  constexpr int SMEM = (NST * STAGE > Out::ELEMS) ? NST * STAGE : Out::ELEMS;
   __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
 
   const int num_m = p.tl->count;
@@ -356,31 +385,34 @@ __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
   };
 
   BTile lb;
-  int64_t b_step;  // element offset of one BK step along K
+  int64_t b_step;  // element offset of one BK_ step along K
   if constexpr (BLAYOUT == B_KCONTIG) {
     lb.init([&](int c) -> const bf16* { return bexp + bcol(c) * p.b_sn; });
-    b_step = BK;
+    b_step = BK_;
   } else {
     lb.init_strided(bexp, p.b_sk, bcol);
-    b_step = static_cast<int64_t>(BK) * p.b_sk;
+    b_step = static_cast<int64_t>(BK_) * p.b_sk;
   }
+  auto issue = [&](int s) {
+    bf16* buf = smem + (s % NST) * STAGE;
+    la.issue(buf, static_cast<int64_t>(s) * BK_);
+    lb.issue(buf + ATile::ELEMS, s * b_step);
+  };
 
   Mma mma;
   mma.zero();
-  const int nk = p.k / BK;
-  la.issue(smem, 0);
-  lb.issue(smem + ATile::ELEMS, 0);
-  wait_loads_and_sync();
+  const int nk = p.k / BK_;
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nk) issue(s);
   for (int kt = 0; kt < nk; ++kt) {
-    bf16* cur = smem + (kt & 1) * STAGE;
-    bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
-    if (kt + 1 < nk) {
-      la.issue(nxt, static_cast<int64_t>(kt + 1) * BK);
-      lb.issue(nxt + ATile::ELEMS, (kt + 1) * b_step);
-    }
-    mma.template compute<ATile, BTile>(cur, cur + ATile::ELEMS, wm, wn, lane);
-    wait_loads_and_sync();
+    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+    __syncthreads();
+    if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    const bf16* cur = smem + (kt % NST) * STAGE;
+    mma.template compute<ATile, BTile, BK_>(cur, cur + ATile::ELEMS, wm, wn, lane);
   }
+  __syncthreads();
 
   // ---- epilogue (LDS-staged, 16-byte stores)
   const int col = lane & 31;
@@ -450,19 +482,30 @@ struct WgradArgs {
   bf16* c;
 };
 
+// Source row of K row r (clamped into the expert) through the optional row
+// table; the table is read through the constant address space so the
+// wave-uniform lookups become scalar loads.
+__device__ __forceinline__ int src_row(const int32_t* table, int r) {
+  return table ? ((const_i32*)(table))[r] : r;
+}
+
 // Scheduling: the (t1, t2) tiles of every expert are split into 8 equal
 // slices and slice x runs on XCD x (workgroup ids congruent to x mod 8), so
 // hot and cold experts are spread evenly over the XCDs whatever the routing
 // skew, while each XCD still sweeps a contiguous, L2-friendly block of one
 // expert's tiles.
-template <int BM, int BN, int WM, int WN>
+// DIRECT = true stores accumulators straight from registers (small-K tiles:
+// LDS stays small so several workgroups per CU overlap their stores).
+template <int BM, int BN, int BK_, int NST, bool DIRECT>
 __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, int num_experts, int per_xcd) {
+  constexpr int WM = 2, WN = 2;
   using Mma = MmaTile<BM, BN, WM, WN>;
-  using PTile = MnTile<BM>;
-  using QTile = MnTile<BN>;
+  using PTile = MnTile<BM, BK_>;
+  using QTile = MnTile<BN, BK_>;
   constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
+  constexpr int LPS = PTile::PER_WAVE + QTile::PER_WAVE;
   using Out = StageOut<BM, BN>;
-  constexpr int SMEM = (2 * STAGE > Out::ELEMS) ? 2 * STAGE : Out::ELEMS;
+  constexpr int SMEM = (DIRECT || NST * STAGE > Out::ELEMS) ? NST * STAGE : Out::ELEMS;
   __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
   const int t1n = a.n1 / BM, t2n = a.n2 / BN;
   const int per_e = t1n * t2n;
@@ -473,73 +516,80 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
   int t1, t2;
   grouped_mn(t, t1n, t2n, t1, t2);
   const int r0 = a.offsets[e], r1 = a.offsets[e + 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-
-  // Source rows of the next K step are resolved one step ahead so the index
-  // loads never stall the copies.
-  int prow[PTile::PER_WAVE], qrow[QTile::PER_WAVE];
-  auto fetch_rows = [&](int k0) {
-#pragma unroll
-    for (int v = 0; v < PTile::PER_WAVE; ++v) {
-      const int r = min(r0 + k0 + PTile::k_of(v), r1 - 1);
-      prow[v] = a.p_rows ? a.p_rows[r] : r;
-    }
-#pragma unroll
-    for (int v = 0; v < QTile::PER_WAVE; ++v) {
-      const int r = min(r0 + k0 + QTile::k_of(v), r1 - 1);
-      qrow[v] = a.q_rows ? a.q_rows[r] : r;
-    }
-  };
   const int64_t pc = static_cast<int64_t>(t1) * BM, qc = static_cast<int64_t>(t2) * BN;
-  auto issue = [&](bf16* buf) {
-    PTile::issue_rows(buf, [&](int v) { return a.p + static_cast<int64_t>(prow[v]) * a.ldp + pc; });
-    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) { return a.q + static_cast<int64_t>(qrow[v]) * a.ldq + qc; });
-  };
-  // After a step's copies landed: zero the K rows past the expert's end.
-  auto fix_tail = [&](bf16* buf, int k0) {
-    const int kv = r1 - r0 - k0;
-    if (kv < BK) {
-      __syncthreads();
-      PTile::zero_tail(buf, kv);
-      QTile::zero_tail(buf + PTile::ELEMS, kv);
-      __syncthreads();
-    }
+
+  // Stage s: K rows [r0 + s*BK_, ...). Each copy instruction of a wave covers
+  // KPC consecutive K rows, so its row lookups are wave-uniform.
+  auto issue = [&](int s) {
+    bf16* buf = smem + (s % NST) * STAGE;
+    const int kbase = r0 + s * BK_;
+    PTile::issue_rows(buf, [&](int v) {
+      const int kc = (v * (kThreads / 64) + wave) * PTile::KPC;
+      int rsel = src_row(a.p_rows, min(kbase + kc, r1 - 1));
+#pragma unroll
+      for (int q = 1; q < PTile::KPC; ++q) {
+        const int rq = src_row(a.p_rows, min(kbase + kc + q, r1 - 1));
+        rsel = ((lane / PTile::VPR) == q) ? rq : rsel;
+      }
+      return a.p + static_cast<int64_t>(rsel) * a.ldp + pc;
+    });
+    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) {
+      const int kc = (v * (kThreads / 64) + wave) * QTile::KPC;
+      int rsel = src_row(a.q_rows, min(kbase + kc, r1 - 1));
+#pragma unroll
+      for (int q = 1; q < QTile::KPC; ++q) {
+        const int rq = src_row(a.q_rows, min(kbase + kc + q, r1 - 1));
+        rsel = ((lane / QTile::VPR) == q) ? rq : rsel;
+      }
+      return a.q + static_cast<int64_t>(rsel) * a.ldq + qc;
+    });
   };
 
   Mma mma;
   mma.zero();
-  const int nk = (r1 - r0 + BK - 1) / BK;
-  if (nk > 0) {
-    fetch_rows(0);
-    issue(smem);
-    if (nk > 1) fetch_rows(BK);
-    wait_loads_and_sync();
-    fix_tail(smem, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      bf16* cur = smem + (kt & 1) * STAGE;
-      bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
-      if (kt + 1 < nk) {
-        issue(nxt);
-        if (kt + 2 < nk) fetch_rows((kt + 2) * BK);
-      }
-      mma.template compute<PTile, QTile>(cur, cur + PTile::ELEMS, wm, wn, lane);
-      wait_loads_and_sync();
-      if (kt + 1 < nk) fix_tail(nxt, (kt + 1) * BK);
+  const int nk = (r1 - r0 + BK_ - 1) / BK_;
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nk) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+    __syncthreads();
+    bf16* cur = smem + (kt % NST) * STAGE;
+    const int kv = r1 - r0 - kt * BK_;
+    if (kv < BK_) {  // ragged tail: zero the K rows past the expert's end
+      PTile::zero_tail(cur, kv);
+      QTile::zero_tail(cur + PTile::ELEMS, kv);
+      __syncthreads();
     }
+    if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    mma.template compute<PTile, QTile, BK_>(cur, cur + PTile::ELEMS, wm, wn, lane);
   }
   const int col = lane & 31;
-  if (nk == 0) __syncthreads();
+  bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + static_cast<int64_t>(t1) * BM * a.n2 + t2 * BN;
+  if constexpr (DIRECT) {
 #pragma unroll
-  for (int i = 0; i < Mma::MI; ++i)
+    for (int i = 0; i < Mma::MI; ++i)
 #pragma unroll
-    for (int jj = 0; jj < Mma::NI; ++jj)
+      for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + jj * 32 + col,
-                 mma.acc[i][jj][r]);
-  Out::flush(smem, BM, a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + static_cast<int64_t>(t1) * BM * a.n2 + t2 * BN,
-             a.n2);
+        for (int r = 0; r < 16; ++r)
+          reinterpret_cast<uint16_t*>(out)[static_cast<int64_t>(wm * Mma::TM + i * 32 + Mma::acc_row(r, lane)) * a.n2 +
+                                           wn * Mma::TN + jj * 32 + col] = f32_to_bf16_bits(mma.acc[i][jj][r]);
+  } else {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < Mma::MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < Mma::NI; ++jj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + jj * 32 + col,
+                   mma.acc[i][jj][r]);
+    Out::flush(smem, BM, out, a.n2);
+  }
 }
 
 // ------------------------------------------------------------------ host side
@@ -571,11 +621,22 @@ RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
   return c;
 }
 
-template <int BM, int BN, int BLAYOUT, int EPI>
+// Pipeline variant of the 256x256 tile: 1 = BK 64 x 2 stages (default,
+// measured faster), 0 = BK 32 x 4 stages (MM_GEMM_PIPE=bk32, for A/B runs).
+int pipe_variant() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("MM_GEMM_PIPE");
+    v = (e && strcmp(e, "bk32") == 0) ? 0 : 1;
+  }
+  return v;
+}
+
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
-  grouped_rows_kernel<BM, BN, 2, 2, BLAYOUT, EPI><<<grid, kThreads, 0, s>>>(p);
+  grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI><<<grid, kThreads, 0, s>>>(p);
 }
 
 template <int BLAYOUT, int EPI>
@@ -584,12 +645,16 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   const RowsCfg c = pick_rows_cfg(max_rows, E, p.n);
   if (int rc = launch_tiles(offsets, E, c.bm, ws, s)) return rc;
   p.tl = static_cast<const TileList*>(ws);
-  if (c.bm == 256)
-    launch_rows_cfg<256, 256, BLAYOUT, EPI>(p, max_rows, E, s);
-  else if (c.bn == 256)
-    launch_rows_cfg<128, 256, BLAYOUT, EPI>(p, max_rows, E, s);
-  else
-    launch_rows_cfg<128, 128, BLAYOUT, EPI>(p, max_rows, E, s);
+  if (c.bm == 256) {
+    if (pipe_variant() == 1)
+      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
+    else
+      launch_rows_cfg<256, 256, 32, 4, BLAYOUT, EPI>(p, max_rows, E, s);
+  } else if (c.bn == 256) {
+    launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
+  } else {
+    launch_rows_cfg<128, 128, 64, 4, BLAYOUT, EPI>(p, max_rows, E, s);
+  }
   return mm_check_launch(what);
 }
 
@@ -674,8 +739,8 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
 
 extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows, const uint16_t* q,
                                 int64_t ldq, const int32_t* q_rows, const int32_t* offsets, int32_t num_experts,
-                                int32_t n1, int32_t n2, uint16_t* c, void* workspace, size_t workspace_bytes,
-                                mm_stream_t stream) {
+                                int64_t max_rows, int32_t n1, int32_t n2, uint16_t* c, void* workspace,
+                                size_t workspace_bytes, mm_stream_t stream) {
   (void)workspace;
   (void)workspace_bytes;
   MM_CHECK_ARG(p && q && offsets && c, "mm_grouped_wgrad: null pointer");
@@ -684,8 +749,12 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   MM_CHECK_ARG(ldp % 8 == 0 && ldq % 8 == 0 && al16(p) && al16(q), "mm_grouped_wgrad: 16-byte alignment required");
   WgradArgs a{reinterpret_cast<const bf16*>(p), ldp, p_rows, reinterpret_cast<const bf16*>(q), ldq,
               q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c)};
-  const int bm = (n1 % 256 == 0) ? 256 : 128;
-  const int bn = (n2 % 256 == 0) ? 256 : 128;
+  MM_CHECK_ARG(max_rows >= 0, "mm_grouped_wgrad: bad max_rows");
+  // Experts averaging <= 128 rows (K of the wgrad GEMM): small tiles with
+  // direct stores, the output write dominates. Otherwise 256-wide tiles.
+  const bool small_k = max_rows <= 128 * static_cast<int64_t>(num_experts);
+  const int bm = (!small_k && n1 % 256 == 0) ? 256 : 128;
+  const int bn = (!small_k && n2 % 256 == 0) ? 256 : 128;
   const int64_t per_e = static_cast<int64_t>(n1 / bm) * (n2 / bn);
   const int64_t per_xcd = (per_e + kXcds - 1) / kXcds;
   const int64_t grid64 = static_cast<int64_t>(num_experts) * per_xcd * kXcds;
@@ -693,13 +762,19 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   const int grid = static_cast<int>(grid64);
   const int px = static_cast<int>(per_xcd);
   hipStream_t s = mm_hip_stream(stream);
-  if (bm == 256 && bn == 256)
-    grouped_wgrad_kernel<256, 256, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
-  else if (bm == 256)
-    grouped_wgrad_kernel<256, 128, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
-  else if (bn == 256)
-    grouped_wgrad_kernel<128, 256, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
-  else
-    grouped_wgrad_kernel<128, 128, 2, 2><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  if (small_k) {
+    grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  } else if (bm == 256 && bn == 256) {
+    if (pipe_variant() == 1)
+      grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    else
+      grouped_wgrad_kernel<256, 256, 32, 4, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  } else if (bm == 256) {
+    grouped_wgrad_kernel<256, 128, 64, 3, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  } else if (bn == 256) {
+    grouped_wgrad_kernel<128, 256, 64, 3, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  } else {
+    grouped_wgrad_kernel<128, 128, 64, 4, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+  }
   return mm_check_launch("mm_grouped_wgrad");
 }

@@ -13,7 +13,7 @@ import os
 
 import torch
 
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmegamoe.so")
+_LIB_PATH = os.environ.get("MEGAMOE_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmegamoe.so")
 
 # Activation kinds (include/megamoe.h MM_ACT_*).
 ACT_KINDS = {"swiglu": 0, "situglu": 1, "clamp_swiglu": 2}
@@ -36,7 +36,7 @@ SIGNATURES = {
                                      _F32, _F32, _F32, _P, _P, _P, _SZ, _P]),
     "mm_grouped_gemm": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _I32,
                                        _I32, _P, _I64, _P, _SZ, _P]),
-    "mm_grouped_wgrad": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I32, _I32, _P, _P,
+    "mm_grouped_wgrad": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _P, _P,
                                         _SZ, _P]),
     "mm_combine": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _I32, _P, _I64, _P]),
     "mm_gather_route_grad": (ctypes.c_int, [_P, _P, _I64, _P, _P]),

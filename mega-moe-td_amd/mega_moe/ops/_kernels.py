@@ -83,16 +83,18 @@ def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_row
     return c
 
 
-def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int) -> torch.Tensor:
+def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int | None = None) -> torch.Tensor:
     """c[e] = P_e^T Q_e over each expert's rows -> [E, n1, n2] bf16."""
     _check_bf16("p", p)
     _check_bf16("q", q)
     if p.stride(1) != 1 or q.stride(1) != 1 or p.shape[1] != n1 or q.shape[1] != n2:
         raise ValueError("grouped_wgrad: p [*, n1], q [*, n2] with unit column stride required")
     num_experts = offsets.numel() - 1
+    if max_rows is None:
+        max_rows = q.shape[0] if q_rows is None else q_rows.shape[0]
     c = torch.empty(num_experts, n1, n2, dtype=torch.bfloat16, device=p.device)
     _lib.call("mm_grouped_wgrad", _lib.ptr(p), p.stride(0), _lib.ptr(p_rows), _lib.ptr(q), q.stride(0),
-              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, n1, n2, _lib.ptr(c), None, 0,
+              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), None, 0,
               _lib.stream_of(p.device))
     return c
 

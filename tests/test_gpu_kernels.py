@@ -130,7 +130,8 @@ def test_grouped_gemm(layout, kind, gather):
 
 @pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
 @pytest.mark.parametrize("gather", [False, True])
-def test_grouped_wgrad(kind, gather):
+@pytest.mark.parametrize("tiling", ["small_k", "large_k"])
+def test_grouped_wgrad(kind, gather, tiling):
     from mega_moe.ops import _kernels as K
     E, N1, N2 = 5, 256, 128
     offs = _ragged(E, kind, seed=4)
@@ -139,7 +140,8 @@ def test_grouped_wgrad(kind, gather):
     p = torch.randn(M + 9, N1, device=DEV, generator=g).to(torch.bfloat16)
     q = torch.randn(M, N2, device=DEV, generator=g).to(torch.bfloat16)
     p_rows = torch.randint(0, M + 9, (M,), device=DEV, dtype=torch.int32, generator=g) if gather else None
-    c = K.grouped_wgrad(p, p_rows, q, None, offs, N1, N2)
+    # max_rows only selects the tiling: 0 forces the small-K variant
+    c = K.grouped_wgrad(p, p_rows, q, None, offs, N1, N2, max_rows=0 if tiling == "small_k" else 1 << 20)
     torch.cuda.synchronize()
     pf = p.float().cpu()
     pf = pf[p_rows.long().cpu()] if gather else pf[:M]
