@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--config", default="e32")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=0, help="token sample for the CPU baseline (0 = auto)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy 5 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -49,17 +51,42 @@ def fc1_algorithmic(spec, save_fc1: bool):
     return flops, byts
 
 
-def cpu_baseline(spec, tokens: int):
+def cpu_inputs(spec, tokens: int, seed: int = 99):
+    """CPU inputs for a token sample: the sample's routing over all E experts,
+    with weights materialised only for the experts the sample touches
+    (renumbered densely), so the per-token CPU work equals the full layer's."""
     import torch
 
-    from mega_moe.bench_configs import make_inputs
+    from mega_moe.bench_configs import CaseSpec, make_routing
+
+    s = CaseSpec(spec.name, tokens, spec.hidden, spec.inter, spec.experts, spec.top_k, spec.routing,
+                 spec.backward, spec.dtype, spec.zipf_s)
+    gen = torch.Generator().manual_seed(seed)
+    sel, rw = make_routing(s, gen)
+    used = torch.unique(sel)
+    remap = torch.full((spec.experts,), -1, dtype=torch.int32)
+    remap[used.long()] = torch.arange(used.numel(), dtype=torch.int32)
+    sel = remap[sel.long()]
+    U, H, I = used.numel(), spec.hidden, spec.inter
+    bf = torch.bfloat16
+    x = torch.randn(tokens, H, generator=gen).to(bf)
+    dy = torch.randn(tokens, H, generator=gen).to(bf)
+    gate_up = (torch.randn(U, H, 2 * I, generator=gen) * 0.02).to(bf)
+    down = (torch.randn(U, I, H, generator=gen) * 0.02).to(bf).transpose(1, 2)
+    return dict(x=x, selected=sel, rw=rw, gate_up=gate_up, down=down, dy=dy), U
+
+
+def cpu_baseline(spec, tokens: int):
+    """Time the CPU restatement of the reference's Torch layer on a token sample."""
+    import torch
+
     sys.path.insert(0, ROOT)
     from oracle import moe_oracle as O
 
     threads = torch.get_num_threads()
-    inp = make_inputs(spec, device="cpu", seed=99, tokens=tokens)
+    inp, used = cpu_inputs(spec, tokens)
     times = []
-    for rep in range(2):
+    for _ in range(2):
         t0 = time.perf_counter()
         out, st = O.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
         if spec.backward:
@@ -73,12 +100,23 @@ def cpu_baseline(spec, tokens: int):
         "cores": threads,
         "kind": "port",
         "sample": f"{spec.name} layer {'fwd+bwd' if spec.backward else 'fwd'} on {tokens} of {spec.tokens} tokens "
-                  f"(all {spec.experts} experts, full H/I), best of 2 runs: {t * 1e3:.0f} ms",
+                  f"({used} experts touched, full H={spec.hidden}/I={spec.inter}), per-expert fp32 matmul loop "
+                  f"with bf16 rounding, best of 2: {t * 1e3:.0f} ms",
     }
 
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        import torch
+
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": 1 << 30, "launches": 5}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported "
                                    "(expert parallelism across GPUs is out of scope)"}))
@@ -146,7 +184,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        toks = args.cpu_tokens or {"toy": 512, "e32": 512, "qwen": 512, "kimi": 8, "skew": 256}[spec.name]
+        toks = args.cpu_tokens or {"toy": 512, "e32": 1024, "qwen": 2048, "kimi": 2, "skew": 512}[spec.name]
         print(f"[bench] cpu baseline on {toks} tokens", file=sys.stderr, flush=True)
         try:
             cpu = cpu_baseline(spec, toks)

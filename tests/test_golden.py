@@ -1,0 +1,54 @@
+"""Committed fixture (tests/golden/layer_small.npz, written by
+tests/golden/make_fixtures.py from the oracle): the oracle must keep
+reproducing it exactly (CPU), and the HIP path must match it (GPU)."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests._numeric import assert_rel
+
+FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layer_small.npz")
+
+
+def load():
+    z = np.load(FIX)
+    bf = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+    return dict(x=bf(z["x"]), selected=torch.from_numpy(z["selected"]), rw=torch.from_numpy(z["rw"]),
+                gate_up=bf(z["gate_up"]), down=bf(z["down"]), dy=bf(z["dy"]), out=bf(z["out"]),
+                grad_hidden=bf(z["grad_hidden"]), grad_routing_weights=torch.from_numpy(z["grad_routing_weights"]),
+                grad_gate_up=bf(z["grad_gate_up"]), grad_fc2=bf(z["grad_fc2"]), send_route=z["send_route"],
+                route_to_send=z["route_to_send"], offsets=z["offsets"])
+
+
+def test_oracle_reproduces_fixture():
+    f = load()
+    out, st = O.forward(f["x"], f["selected"], f["gate_up"], f["down"], f["rw"])
+    g = O.backward(st, f["dy"])
+    assert np.array_equal(st["tables"]["send_route"], f["send_route"])
+    assert np.array_equal(st["tables"]["route_to_send"], f["route_to_send"])
+    assert torch.equal(out, f["out"])
+    for k in ("grad_hidden", "grad_routing_weights", "grad_gate_up", "grad_fc2"):
+        assert torch.equal(g[k], f[k]), k
+
+
+@pytest.mark.gpu
+def test_hip_path_matches_fixture():
+    import mega_moe
+    f = load()
+    d = {k: v.cuda() for k, v in f.items() if isinstance(v, torch.Tensor)}
+    T, H = d["x"].shape
+    E, k = d["gate_up"].shape[0], d["selected"].shape[1]
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=T, hidden_size=H, top_k=k, num_experts=E)
+    out, saved = op.forward(d["x"], d["selected"], d["gate_up"], d["down"], d["rw"], return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, d["dy"])
+    torch.cuda.synchronize()
+    nv = int(f["offsets"][-1])
+    assert np.array_equal(saved["send_route_indices"][:nv].cpu().numpy(), f["send_route"])
+    assert np.array_equal(saved["route_to_send"].cpu().numpy(), f["route_to_send"])
+    assert_rel(out, f["out"], 2e-2, "out")
+    for key in ("grad_hidden", "grad_routing_weights", "grad_gate_up", "grad_fc2"):
+        assert_rel(g[key], f[key], 2e-2, key)
