@@ -267,18 +267,28 @@ struct MmaTile {
     __builtin_amdgcn_iglp_opt(MM_IGLP);
 #endif
     bf16x8 a[2][MI], b[2][NI];
+#ifdef MM_DIAG_NOA
+#define MM_AFRAG(r0, kk) (bf16x8{})
+#else
+#define MM_AFRAG(r0, kk) ATile::frag(As, r0, kk, lane)
+#endif
+#ifdef MM_DIAG_NOB
+#define MM_BFRAG(r0, kk) (bf16x8{})
+#else
+#define MM_BFRAG(r0, kk) BTile::frag(Bs, r0, kk, lane)
+#endif
 #pragma unroll
-    for (int i = 0; i < MI; ++i) a[0][i] = ATile::frag(As, wm * TM + i * 32, 0, lane);
+    for (int i = 0; i < MI; ++i) a[0][i] = MM_AFRAG(wm * TM + i * 32, 0);
 #pragma unroll
-    for (int j = 0; j < NI; ++j) b[0][j] = BTile::frag(Bs, wn * TN + j * 32, 0, lane);
+    for (int j = 0; j < NI; ++j) b[0][j] = MM_BFRAG(wn * TN + j * 32, 0);
 #pragma unroll
     for (int s = 0; s < BK_ / 16; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
       if (s + 1 < BK_ / 16) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i) a[nxt][i] = ATile::frag(As, wm * TM + i * 32, (s + 1) * 16, lane);
+        for (int i = 0; i < MI; ++i) a[nxt][i] = MM_AFRAG(wm * TM + i * 32, (s + 1) * 16);
 #pragma unroll
-        for (int j = 0; j < NI; ++j) b[nxt][j] = BTile::frag(Bs, wn * TN + j * 32, (s + 1) * 16, lane);
+        for (int j = 0; j < NI; ++j) b[nxt][j] = MM_BFRAG(wn * TN + j * 32, (s + 1) * 16);
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
@@ -482,13 +492,6 @@ struct WgradArgs {
   bf16* c;
 };
 
-// Source row of K row r (clamped into the expert) through the optional row
-// table; the table is read through the constant address space so the
-// wave-uniform lookups become scalar loads.
-__device__ __forceinline__ int src_row(const int32_t* table, int r) {
-  return table ? ((const_i32*)(table))[r] : r;
-}
-
 // Scheduling: the (t1, t2) tiles of every expert are split into 8 equal
 // slices and slice x runs on XCD x (workgroup ids congruent to x mod 8), so
 // hot and cold experts are spread evenly over the XCDs whatever the routing
@@ -503,7 +506,6 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
   using PTile = MnTile<BM, BK_>;
   using QTile = MnTile<BN, BK_>;
   constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
-  constexpr int LPS = PTile::PER_WAVE + QTile::PER_WAVE;
   using Out = StageOut<BM, BN>;
   constexpr int SMEM = (DIRECT || NST * STAGE > Out::ELEMS) ? NST * STAGE : Out::ELEMS;
   __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
@@ -521,41 +523,39 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
   const int wm = wave / WN, wn = wave % WN;
   const int64_t pc = static_cast<int64_t>(t1) * BM, qc = static_cast<int64_t>(t2) * BN;
 
-  // Stage s: K rows [r0 + s*BK_, ...). Each copy instruction of a wave covers
-  // KPC consecutive K rows, so its row lookups are wave-uniform.
+  // Source rows of a stage are looked up one stage ahead (ordinary vector
+  // loads); with the 2-stage ring their wait coincides with the stage wait.
+  int prow[PTile::PER_WAVE], qrow[QTile::PER_WAVE];
+  auto fetch_rows = [&](int s) {
+    const int kbase = r0 + s * BK_;
+#pragma unroll
+    for (int v = 0; v < PTile::PER_WAVE; ++v) {
+      const int r = min(kbase + PTile::k_of(v), r1 - 1);
+      prow[v] = a.p_rows ? a.p_rows[r] : r;
+    }
+#pragma unroll
+    for (int v = 0; v < QTile::PER_WAVE; ++v) {
+      const int r = min(kbase + QTile::k_of(v), r1 - 1);
+      qrow[v] = a.q_rows ? a.q_rows[r] : r;
+    }
+  };
   auto issue = [&](int s) {
     bf16* buf = smem + (s % NST) * STAGE;
-    const int kbase = r0 + s * BK_;
-    PTile::issue_rows(buf, [&](int v) {
-      const int kc = (v * (kThreads / 64) + wave) * PTile::KPC;
-      int rsel = src_row(a.p_rows, min(kbase + kc, r1 - 1));
-#pragma unroll
-      for (int q = 1; q < PTile::KPC; ++q) {
-        const int rq = src_row(a.p_rows, min(kbase + kc + q, r1 - 1));
-        rsel = ((lane / PTile::VPR) == q) ? rq : rsel;
-      }
-      return a.p + static_cast<int64_t>(rsel) * a.ldp + pc;
-    });
-    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) {
-      const int kc = (v * (kThreads / 64) + wave) * QTile::KPC;
-      int rsel = src_row(a.q_rows, min(kbase + kc, r1 - 1));
-#pragma unroll
-      for (int q = 1; q < QTile::KPC; ++q) {
-        const int rq = src_row(a.q_rows, min(kbase + kc + q, r1 - 1));
-        rsel = ((lane / QTile::VPR) == q) ? rq : rsel;
-      }
-      return a.q + static_cast<int64_t>(rsel) * a.ldq + qc;
-    });
+    PTile::issue_rows(buf, [&](int v) { return a.p + static_cast<int64_t>(prow[v]) * a.ldp + pc; });
+    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) { return a.q + static_cast<int64_t>(qrow[v]) * a.ldq + qc; });
   };
 
   Mma mma;
   mma.zero();
   const int nk = (r1 - r0 + BK_ - 1) / BK_;
-#pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
-    if (s < nk) issue(s);
+  static_assert(NST == 2, "wgrad row-index prefetch assumes a 2-stage ring");
+  if (nk > 0) {
+    fetch_rows(0);
+    issue(0);
+    if (nk > 1) fetch_rows(1);
+  }
   for (int kt = 0; kt < nk; ++kt) {
-    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+    wait_vmcnt<0>();
     __syncthreads();
     bf16* cur = smem + (kt % NST) * STAGE;
     const int kv = r1 - r0 - kt * BK_;
@@ -564,7 +564,10 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
       QTile::zero_tail(cur + PTile::ELEMS, kv);
       __syncthreads();
     }
-    if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    if (kt + 1 < nk) {
+      issue(kt + 1);
+      if (kt + 2 < nk) fetch_rows(kt + 2);
+    }
     mma.template compute<PTile, QTile, BK_>(cur, cur + PTile::ELEMS, wm, wn, lane);
   }
   const int col = lane & 31;
@@ -765,16 +768,13 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   if (small_k) {
     grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256 && bn == 256) {
-    if (pipe_variant() == 1)
-      grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
-    else
-      grouped_wgrad_kernel<256, 256, 32, 4, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256) {
-    grouped_wgrad_kernel<256, 128, 64, 3, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    grouped_wgrad_kernel<256, 128, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bn == 256) {
-    grouped_wgrad_kernel<128, 256, 64, 3, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    grouped_wgrad_kernel<128, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else {
-    grouped_wgrad_kernel<128, 128, 64, 4, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    grouped_wgrad_kernel<128, 128, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   }
   return mm_check_launch("mm_grouped_wgrad");
 }

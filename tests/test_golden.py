@@ -30,9 +30,11 @@ def test_oracle_reproduces_fixture():
     g = O.backward(st, f["dy"])
     assert np.array_equal(st["tables"]["send_route"], f["send_route"])
     assert np.array_equal(st["tables"]["route_to_send"], f["route_to_send"])
-    assert torch.equal(out, f["out"])
+    # values: CPU BLAS accumulation order differs between machines, which can
+    # flip a bf16 rounding; the fixture is matched to well under the bar
+    assert_rel(out, f["out"], 1e-2, "out")
     for k in ("grad_hidden", "grad_routing_weights", "grad_gate_up", "grad_fc2"):
-        assert torch.equal(g[k], f[k]), k
+        assert_rel(g[k], f[k], 1e-2, k)
 
 
 @pytest.mark.gpu
