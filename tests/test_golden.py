@@ -1,6 +1,7 @@
 """Committed fixture (tests/golden/layer_small.npz, written by
 tests/golden/make_fixtures.py from the oracle): the oracle must keep
-reproducing it exactly (CPU), and the HIP path must match it (GPU)."""
+reproducing it (routing exactly, values to 1e-2: CPU BLAS summation order
+differs across hosts), and the HIP path must match it (GPU)."""
 
 import os
 
