@@ -497,8 +497,10 @@ struct WgradArgs {
 // hot and cold experts are spread evenly over the XCDs whatever the routing
 // skew, while each XCD still sweeps a contiguous, L2-friendly block of one
 // expert's tiles.
-// DIRECT = true stores accumulators straight from registers (small-K tiles:
-// LDS stays small so several workgroups per CU overlap their stores).
+// DIRECT = true (small-K tiles): the output tile is staged in the stage
+// buffers themselves (XOR-swizzled, unpadded) instead of a separate padded
+// region, so LDS stays at 2 stages and several workgroups per CU overlap
+// their 16-byte stores.
 template <int BM, int BN, int BK_, int NST, bool DIRECT>
 __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, int num_experts, int per_xcd) {
   constexpr int WM = 2, WN = 2;
@@ -573,14 +575,28 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
   const int col = lane & 31;
   bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + static_cast<int64_t>(t1) * BM * a.n2 + t2 * BN;
   if constexpr (DIRECT) {
+    // stage the tile unpadded in the (now idle) stage buffers, 16-byte
+    // vector slot v of row r at v ^ (r & 7), then 16-byte stores
+    static_assert(BM * BN <= NST * STAGE, "staging must fit the stage buffers");
+    constexpr int VPR = BN / 8;
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < Mma::MI; ++i)
 #pragma unroll
       for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          reinterpret_cast<uint16_t*>(out)[static_cast<int64_t>(wm * Mma::TM + i * 32 + Mma::acc_row(r, lane)) * a.n2 +
-                                           wn * Mma::TN + jj * 32 + col] = f32_to_bf16_bits(mma.acc[i][jj][r]);
+        for (int r = 0; r < 16; ++r) {
+          const int tr = wm * Mma::TM + i * 32 + Mma::acc_row(r, lane);
+          const int tc = wn * Mma::TN + jj * 32 + col;
+          reinterpret_cast<uint16_t*>(smem)[tr * BN + ((((tc >> 3) ^ (tr & 7)) << 3) | (tc & 7))] =
+              f32_to_bf16_bits(mma.acc[i][jj][r]);
+        }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+      const int r = idx / VPR, cv = idx % VPR;
+      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * a.n2 + cv * 8) =
+          *reinterpret_cast<const uint4*>(smem + r * BN + ((cv ^ (r & 7)) << 3));
+    }
   } else {
     __syncthreads();
 #pragma unroll
