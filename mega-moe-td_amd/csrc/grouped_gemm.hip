@@ -144,13 +144,13 @@ __device__ __forceinline__ v4i16 lds_read_tr16(const bf16* p) {
 // 64-byte rows swz = (r >> 1) & 3, so the 8 rows touched by one pass of a
 // 16-byte fragment read land in distinct banks. Rows outside the tile point
 // at a valid row; their products are never stored.
-template <int ROWS, int BK_>
+template <int ROWS, int BK_, int NT = kThreads>
 struct KcTile {
   static constexpr int ELEMS = ROWS * BK_;
   static constexpr int VPR = BK_ / 8;                      // vectors per row
   static constexpr int CHUNKS = ELEMS / kChunkElems;       // 1 KiB chunks per K step
-  static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
-  static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
+  static constexpr int PER_WAVE = CHUNKS / (NT / 64);
+  static_assert(PER_WAVE * (NT / 64) == CHUNKS, "chunks/waves mismatch");
   const bf16* ptr[PER_WAVE];
 
   __device__ static int swz(int r) { return VPR == 8 ? (r & 7) : ((r >> 1) & 3); }
@@ -160,7 +160,7 @@ struct KcTile {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v) {
-      const int q = (v * (kThreads / 64) + wave) * 64 + lane;
+      const int q = (v * (NT / 64) + wave) * 64 + lane;
       const int r = q / VPR;
       ptr[v] = row_ptr(r) + ((q % VPR) ^ swz(r)) * 8;
     }
@@ -168,7 +168,7 @@ struct KcTile {
   __device__ void issue(bf16* lds, int64_t k0) const {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + k0, lds + (v * (kThreads / 64) + wave) * kChunkElems);
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + k0, lds + (v * (NT / 64) + wave) * kChunkElems);
   }
   // MFMA 32x32x16 operand: row r0 + lane%32, k = kk + 8*(lane/32) .. +8
   __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
@@ -185,23 +185,23 @@ __device__ __forceinline__ int mn_swz(int k) { return (0xEA40 >> ((k & 3) * 4)) 
 
 // M/N-contiguous operand: LDS [BK_][ROWS] in the source's natural layout
 // (swizzled); MFMA fragments are read with the transposing LDS read.
-template <int ROWS, int BK_>
+template <int ROWS, int BK_, int NT = kThreads>
 struct MnTile {
   static constexpr int ELEMS = BK_ * ROWS;
   static constexpr int VPR = ROWS / 8;                      // 16-byte vectors per K row
   static constexpr int CHUNKS = ELEMS / kChunkElems;
-  static constexpr int PER_WAVE = CHUNKS / (kThreads / 64);
+  static constexpr int PER_WAVE = CHUNKS / (NT / 64);
   static constexpr int KPC = 64 / VPR;                      // K rows per 1 KiB chunk
-  static_assert(PER_WAVE * (kThreads / 64) == CHUNKS, "chunks/waves mismatch");
+  static_assert(PER_WAVE * (NT / 64) == CHUNKS, "chunks/waves mismatch");
   static_assert(VPR >= 16, "swizzle needs >= 16 vectors per row");
   const bf16* ptr[PER_WAVE];
 
   // K row and source column (elements) this lane copies in instruction v.
   __device__ static int k_of(int v) {
-    return ((v * (kThreads / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)) / VPR;
+    return ((v * (NT / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)) / VPR;
   }
   __device__ static int col_of(int v) {
-    const int q = (v * (kThreads / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
+    const int q = (v * (NT / 64) + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63);
     return ((q % VPR) ^ mn_swz(q / VPR)) * 8;
   }
   // Fixed-stride source: element (k, c) at base + k*ld + col_off(c).
@@ -213,7 +213,7 @@ struct MnTile {
   __device__ void issue(bf16* lds, int64_t off) const {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + off, lds + (v * (kThreads / 64) + wave) * kChunkElems);
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + off, lds + (v * (NT / 64) + wave) * kChunkElems);
   }
   // Per-vector source (wgrad): src(v) -> row pointer (column 0 of the tile)
   // for the K row this lane copies in instruction v.
@@ -222,7 +222,7 @@ struct MnTile {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v)
-      copy16_to_lds(src(v) + col_of(v), lds + (v * (kThreads / 64) + wave) * kChunkElems);
+      copy16_to_lds(src(v) + col_of(v), lds + (v * (NT / 64) + wave) * kChunkElems);
   }
   __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
     const int s = lane & 15, g = lane >> 4;
@@ -237,7 +237,7 @@ struct MnTile {
   }
   // Zero K rows [k_valid, BK_) of a filled tile (ragged K tail).
   __device__ static void zero_tail(bf16* lds, int k_valid) {
-    for (int i = threadIdx.x; i < (BK_ - k_valid) * VPR; i += kThreads)
+    for (int i = threadIdx.x; i < (BK_ - k_valid) * VPR; i += NT)
       reinterpret_cast<uint4*>(lds + k_valid * ROWS)[i] = make_uint4(0, 0, 0, 0);
   }
 };
@@ -247,7 +247,6 @@ template <int BM, int BN, int WM, int WN>
 struct MmaTile {
   static constexpr int TM = BM / WM, TN = BN / WN;
   static constexpr int MI = TM / 32, NI = TN / 32;
-  static_assert(WM * WN == kThreads / 64, "4 waves per workgroup");
   f32x16 acc[MI][NI];
 
   __device__ void zero() {
@@ -306,7 +305,7 @@ struct MmaTile {
 // Epilogue staging: a BM x NC bf16 tile is written to LDS ([BM][NC+8], the
 // padding keeps the two half-waves of a store on different banks), then
 // copied out row by row with 16-byte global stores; rows >= rows are skipped.
-template <int BM, int NC>
+template <int BM, int NC, int NT = kThreads>
 struct StageOut {
   static constexpr int PITCH = NC + 8;
   static constexpr int ELEMS = BM * PITCH;
@@ -317,7 +316,7 @@ struct StageOut {
   __device__ static void flush(const bf16* lds, int rows, bf16* out, int64_t ld) {
     __syncthreads();
     constexpr int VPR = NC / 8;
-    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
       const int r = idx / VPR, cv = idx % VPR;
       if (r < rows)
         *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * ld + cv * 8) =
@@ -350,16 +349,16 @@ enum { B_KCONTIG = 0, B_NCONTIG = 1 };
 
 // NST-stage ring of LDS buffers: stage s is copied into buffer s % NST while
 // the MFMAs consume stage s - NST + 1; one barrier per K step.
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI>
-__global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
-  constexpr int WM = 2, WN = 2;
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads>
+__global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
+  constexpr int WN = 2, WM = NT / 64 / WN;  // 4 waves: 2x2, 8 waves: 4x2
   using Mma = MmaTile<BM, BN, WM, WN>;
-  using ATile = KcTile<BM, BK_>;
-  using BTile = typename std::conditional<BLAYOUT == B_KCONTIG, KcTile<BN, BK_>, MnTile<BN, BK_>>::type;
+  using ATile = KcTile<BM, BK_, NT>;
+  using BTile = typename std::conditional<BLAYOUT == B_KCONTIG, KcTile<BN, BK_, NT>, MnTile<BN, BK_, NT>>::type;
   static_assert(EPI != EPI_GATED || (Mma::NI % 2 == 0 && BLAYOUT == B_NCONTIG), "gated epilogue layout");
   constexpr int STAGE = ATile::ELEMS + BTile::ELEMS;
   constexpr int LPS = ATile::PER_WAVE + BTile::PER_WAVE;  // copies per wave per stage
-  using Out = StageOut<BM, BN>;
+  using Out = StageOut<BM, BN, NT>;
   constexpr int SMEM = (NST * STAGE > Out::ELEMS) ? NST * STAGE : Out::ELEMS;
   __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
 
@@ -452,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void grouped_rows_kernel(RowsArgs p) {
     __syncthreads();
     constexpr int VPR = BN / 16;  // 8-column vectors per output row
     const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
-    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
       const int r = idx / VPR, cv = idx % VPR;
       if (r >= rows) continue;
       const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
@@ -501,14 +500,14 @@ struct WgradArgs {
 // buffers themselves (XOR-swizzled, unpadded) instead of a separate padded
 // region, so LDS stays at 2 stages and several workgroups per CU overlap
 // their 16-byte stores.
-template <int BM, int BN, int BK_, int NST, bool DIRECT>
-__global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, int num_experts, int per_xcd) {
-  constexpr int WM = 2, WN = 2;
+template <int BM, int BN, int BK_, int NST, bool DIRECT, int NT = kThreads>
+__global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_experts, int per_xcd) {
+  constexpr int WN = 2, WM = NT / 64 / WN;
   using Mma = MmaTile<BM, BN, WM, WN>;
-  using PTile = MnTile<BM, BK_>;
-  using QTile = MnTile<BN, BK_>;
+  using PTile = MnTile<BM, BK_, NT>;
+  using QTile = MnTile<BN, BK_, NT>;
   constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
-  using Out = StageOut<BM, BN>;
+  using Out = StageOut<BM, BN, NT>;
   constexpr int SMEM = (DIRECT || NST * STAGE > Out::ELEMS) ? NST * STAGE : Out::ELEMS;
   __shared__ __attribute__((aligned(1024))) bf16 smem[SMEM];
   const int t1n = a.n1 / BM, t2n = a.n2 / BN;
@@ -592,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void grouped_wgrad_kernel(WgradArgs a, in
               f32_to_bf16_bits(mma.acc[i][jj][r]);
         }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < BM * VPR; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
       const int r = idx / VPR, cv = idx % VPR;
       *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * a.n2 + cv * 8) =
           *reinterpret_cast<const uint4*>(smem + r * BN + ((cv ^ (r & 7)) << 3));
@@ -651,11 +650,23 @@ int pipe_variant() {
   return v;
 }
 
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI>
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
-  grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI><<<grid, kThreads, 0, s>>>(p);
+  grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT><<<grid, NT, 0, s>>>(p);
+}
+
+// 8 waves (2 per SIMD) per 256-row workgroup by default: a second wave on
+// each SIMD keeps the matrix core busy across the other's LDS waits and
+// barriers (measured +10% over 4 waves). MM_GEMM_WAVES=4 selects 4 waves.
+int eight_waves() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("MM_GEMM_WAVES");
+    v = (e && strcmp(e, "4") == 0) ? 0 : 1;
+  }
+  return v;
 }
 
 template <int BLAYOUT, int EPI>
@@ -665,12 +676,17 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   if (int rc = launch_tiles(offsets, E, c.bm, ws, s)) return rc;
   p.tl = static_cast<const TileList*>(ws);
   if (c.bm == 256) {
-    if (pipe_variant() == 1)
+    if (eight_waves())
+      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+    else if (pipe_variant() == 1)
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
     else
       launch_rows_cfg<256, 256, 32, 4, BLAYOUT, EPI>(p, max_rows, E, s);
   } else if (c.bn == 256) {
-    launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
+    if (eight_waves() && getenv("MM_GEMM_MED8"))
+      launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+    else
+      launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
   } else {
     launch_rows_cfg<128, 128, 64, 4, BLAYOUT, EPI>(p, max_rows, E, s);
   }
@@ -784,7 +800,10 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   if (small_k) {
     grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256 && bn == 256) {
-    grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    if (eight_waves())
+      grouped_wgrad_kernel<256, 256, 64, 2, false, 512><<<grid, 512, 0, s>>>(a, num_experts, px);
+    else
+      grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256) {
     grouped_wgrad_kernel<256, 128, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bn == 256) {
