@@ -184,7 +184,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        toks = args.cpu_tokens or {"toy": 512, "e32": 1024, "qwen": 2048, "kimi": 2, "skew": 512}[spec.name]
+        toks = args.cpu_tokens or {"toy": 512, "e32": 4096, "qwen": 2048, "kimi": 2, "skew": 512}[spec.name]
         print(f"[bench] cpu baseline on {toks} tokens", file=sys.stderr, flush=True)
         try:
             cpu = cpu_baseline(spec, toks)
