@@ -1,0 +1,93 @@
+"""Host-side API behaviour of the mega_moe mirror (no GPU needed): the
+reference's validation rules and error types (src/mega_moe/config.py:196-386,
+ops/forward.py:78-243, 766-850, 2112-2137)."""
+
+import pytest
+import torch
+
+import mega_moe
+from mega_moe import MoEForwardConfig, pack_gate_up_weights
+
+
+def test_public_names():
+    for name in ("FusedMoEForward", "DispatchFC1Result", "pack_gate_up_weights", "MegaMoEBackwardFunction",
+                 "MegaMoEFunction", "moe_backward_triton", "MoEForwardConfig", "MoERoutingPlan"):
+        assert hasattr(mega_moe, name)
+
+
+@pytest.mark.parametrize("kw, exc", [
+    (dict(dispatch_fc1_block_size_m=24), ValueError),
+    (dict(fc1_gemm_block_size_n=8), ValueError),
+    (dict(activation="gelu"), ValueError),
+    (dict(situ_beta=0.0), ValueError),
+    (dict(situ_beta="1"), TypeError),
+    (dict(situ_linear_beta=-1.0), ValueError),
+    (dict(clamp_limit=0), ValueError),
+    (dict(save_fc1_dtype="fp32"), ValueError),
+    (dict(receive_capacity_factor=0.5), ValueError),
+    (dict(single_kernel_group_windows=3), ValueError),
+    (dict(enable_moonep=1), TypeError),
+    (dict(enable_single_kernel_forward=True, fc1_gemm_block_size_m=128), ValueError),
+])
+def test_config_validation(kw, exc):
+    with pytest.raises(exc):
+        MoEForwardConfig(**kw)
+
+
+def test_config_defaults():
+    c = MoEForwardConfig()
+    assert c.activation == "swiglu" and c.single_kernel_group_windows == 32
+    assert c.num_aicore_programs > 0 and c.resolved_receive_capacity_factor(4) == 4.0
+    assert MoEForwardConfig(receive_capacity_factor=2).resolved_receive_capacity_factor(8) == 2.0
+
+
+@pytest.mark.parametrize("kw", [
+    dict(max_tokens_per_rank=0), dict(hidden_size=0), dict(top_k=0), dict(num_experts=0)])
+def test_constructor_rejects_nonpositive(kw):
+    base = dict(max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4)
+    base.update(kw)
+    with pytest.raises(ValueError):
+        mega_moe.FusedMoEForward(None, **base)
+
+
+def test_constructor_type_and_unbuilt_features():
+    with pytest.raises(TypeError):
+        mega_moe.FusedMoEForward(None, max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4, config={})
+    with pytest.raises(NotImplementedError):
+        mega_moe.FusedMoEForward(None, max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4,
+                                 config=MoEForwardConfig(enable_moonep=True))
+
+
+def test_pack_gate_up_weights():
+    g = torch.randn(3, 5, 7).to(torch.bfloat16)
+    u = torch.randn(3, 5, 7).to(torch.bfloat16)
+    packed = pack_gate_up_weights(g, u)
+    assert packed.shape == (3, 7, 10) and packed.is_contiguous()
+    assert torch.equal(packed[:, :, :5], g.transpose(1, 2)) and torch.equal(packed[:, :, 5:], u.transpose(1, 2))
+    with pytest.raises(ValueError):
+        pack_gate_up_weights(g, u[:, :4])
+    with pytest.raises(TypeError):
+        pack_gate_up_weights(g.float(), u)
+    with pytest.raises(ValueError):
+        pack_gate_up_weights(g[0], u[0])
+
+
+def test_forward_rejects_host_tensors():
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4)
+    sel = torch.zeros(8, 2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="device"):
+        op.build_routing_plan(sel)
+    with pytest.raises(TypeError):
+        op.build_routing_plan(sel.long())
+    with pytest.raises(ValueError, match="top_k"):
+        op.build_routing_plan(torch.zeros(8, 3, dtype=torch.int32))
+    # reference order (forward.py:766-792): the device check precedes the capacity check
+    with pytest.raises(ValueError, match="device"):
+        op.build_routing_plan(torch.zeros(9, 2, dtype=torch.int32))
+
+
+def test_backward_requires_saved_activations():
+    with pytest.raises(ValueError, match="fc1_output"):
+        mega_moe.moe_backward_triton({}, torch.zeros(1, 1))
+    with pytest.raises(NotImplementedError):
+        mega_moe.moe_backward_triton({"fc1_output": None}, torch.zeros(1, 1), grad_transport=object())

@@ -125,3 +125,58 @@ def test_full_size_sampled_parity(name):
     assert_rel(out[toks], sub, 2e-2, f"{name} sampled rows")
     del inp, out
     torch.cuda.empty_cache()
+
+
+def test_validation_errors_on_device():
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=1)
+    op = _op(spec)
+    x, sel, w1, w2, rw = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"]
+    with pytest.raises(ValueError, match="max_tokens_per_rank"):
+        op.forward(torch.cat([x, x]), torch.cat([sel, sel]), w1, w2, torch.cat([rw, rw]))
+    with pytest.raises(TypeError):
+        op.forward(x.float(), sel, w1, w2, rw)
+    with pytest.raises(ValueError):
+        op.forward(x, sel, w1, w2, rw.to(torch.bfloat16))
+    with pytest.raises(ValueError):
+        op.forward(x, sel, w1[:, :, :-2].contiguous(), w2, rw)
+    with pytest.raises(ValueError):
+        op.forward(x[:, :128].contiguous(), sel, w1, w2, rw)
+    with pytest.raises(ValueError, match="contiguous"):
+        op.forward(x, sel, w1.transpose(1, 2), w2, rw)
+    # single-stream rule (reference forward.py:1929-1936)
+    op.forward(x, sel, w1, w2, rw)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with pytest.raises(RuntimeError, match="single-stream"):
+            op.forward(x, sel, w1, w2, rw)
+    torch.cuda.synchronize()
+
+
+def test_empty_batch():
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=1)
+    op = _op(spec)
+    x0 = inp["x"][:0]
+    out = op.forward(x0, inp["selected"][:0], inp["gate_up"], inp["down"], inp["rw"][:0])
+    assert out.shape == (0, spec.hidden)
+
+
+def test_all_routes_dropped_and_one_hot_expert():
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=4, weight_scale=0.1)
+    op = _op(spec)
+    dropped = torch.full_like(inp["selected"], spec.experts)
+    out = op.forward(inp["x"], dropped, inp["gate_up"], inp["down"], inp["rw"])
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out) == 0
+    hot = torch.zeros_like(inp["selected"])  # every route to expert 0 (reference all-to-rank-0 case)
+    hot[:, 1:] = -1
+    out, saved = op.forward(inp["x"], hot, inp["gate_up"], inp["down"], inp["rw"], return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, inp["dy"])
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), hot.cpu(), inp["gate_up"].cpu(), inp["down"].cpu(), inp["rw"].cpu())
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out, ref_out, 2e-2, "out")
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
+        assert_rel(g[name], ref[name], 2e-2, name)
