@@ -129,10 +129,18 @@ int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows,
  *   c[e, n1, n2] = sum_{i in rows(e)} p[prow(i), n1] * q[qrow(i), n2]
  * prow(i) = p_rows[i] if p_rows != NULL else i (same for q). Output bf16
  * [E, N1, N2] contiguous; experts with no rows get zeros. max_rows is the
- * row capacity (an upper bound of offsets[E]); it only selects the tiling.
+ * row capacity (an upper bound of offsets[E]); it selects the tiling. When
+ * experts average <= 128 rows the output write dominates and a streaming
+ * kernel runs over contiguous operands: gathered ones (p_rows / q_rows) are
+ * first permuted into the workspace, which needs
+ * mm_wgrad_workspace_bytes(max_rows, E, n1, n2) bytes (a smaller or NULL
+ * workspace selects a slower kernel that gathers in place).
  * Replaces kernels/transposed_grouped_gemm.py:24-100 and the default
  * torch_npu grouped wgrad of ops/backward.py:85-94.
  */
+size_t mm_wgrad_workspace_bytes(int64_t max_rows, int32_t num_experts,
+                                int32_t n1, int32_t n2);
+
 int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows,
                      const uint16_t* q, int64_t ldq, const int32_t* q_rows,
                      const int32_t* offsets, int32_t num_experts,

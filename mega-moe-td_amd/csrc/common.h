@@ -30,14 +30,19 @@ static inline hipStream_t mm_hip_stream(mm_stream_t s) { return reinterpret_cast
 static inline size_t mm_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // ---------------------------------------------------------------- bf16
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), bit exact with
-// torch's float->bfloat16 conversion.
+// Round-to-nearest-even fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32: equal
+// to torch's float->bfloat16 conversion for every non-NaN input (NaN stays a
+// quiet NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  uint32_t lsb = (u >> 16) & 1u;
-  u += 0x7fffu + lsb;
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {

@@ -127,7 +127,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // wait until at most n * PER vector-memory ops of this wave are in flight
 template <int PER, int MAXN>
 __device__ __forceinline__ void wait_stages(int n) {
-  if constexpr (MAXN >= 3) { if (n >= 3) { wait_vmcnt<3 * PER>(); return; } }
+  if constexpr (MAXN >= 5) { if (n >= 5) { wait_vmcnt<5 * PER>(); return; } }
+  if constexpr (MAXN >= 4) { if (n == 4) { wait_vmcnt<4 * PER>(); return; } }
+  if constexpr (MAXN >= 3) { if (n == 3 || (MAXN == 3 && n > 3)) { wait_vmcnt<3 * PER>(); return; } }
   if constexpr (MAXN >= 2) { if (n == 2) { wait_vmcnt<2 * PER>(); return; } }
   if constexpr (MAXN >= 1) { if (n == 1) { wait_vmcnt<PER>(); return; } }
   wait_vmcnt<0>();
@@ -479,6 +481,14 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
 }
 
 // ------------------------------------------------------------------ wgrad
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte non-temporal store of an output vector of the weight gradient
+// (streamed out; it is not read again by this pass).
+__device__ __forceinline__ void store_out16(bf16* dst, uint4 v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(dst));
+}
+
 struct WgradArgs {
   const bf16* p;
   int64_t ldp;
@@ -489,6 +499,7 @@ struct WgradArgs {
   const int32_t* offsets;
   int n1, n2;
   bf16* c;
+  int rows_cap;  // row capacity (max_rows): rows at or past it are never read
 };
 
 // Scheduling: the (t1, t2) tiles of every expert are split into 8 equal
@@ -593,8 +604,8 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
     __syncthreads();
     for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
       const int r = idx / VPR, cv = idx % VPR;
-      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(r) * a.n2 + cv * 8) =
-          *reinterpret_cast<const uint4*>(smem + r * BN + ((cv ^ (r & 7)) << 3));
+      store_out16(out + static_cast<int64_t>(r) * a.n2 + cv * 8,
+                  *reinterpret_cast<const uint4*>(smem + r * BN + ((cv ^ (r & 7)) << 3)));
     }
   } else {
     __syncthreads();
@@ -607,6 +618,107 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
           Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + jj * 32 + col,
                    mma.acc[i][jj][r]);
     Out::flush(smem, BM, out, a.n2);
+  }
+}
+
+// ------------------------------------------------------------------ small-K wgrad
+//
+// Weight gradient when experts hold few rows (K of the GEMM; e.g. 73 rows
+// per expert at 4096 tokens, top-16 over 896 experts): the E x n1 x n2 bf16
+// output write dominates.
+__device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
+
+// One BM x BN output tile per workgroup over contiguous operands (gathered
+// operands are permuted into the workspace first by the host side).
+//  * The product is formed transposed, C^T = Q^T P, so each lane's
+//    accumulator holds 4 consecutive output columns of one output row: every
+//    wave stages its sub-tile 64 columns at a time in its own slice of the
+//    (then idle) stage buffers with 8-byte LDS writes and writes it back as
+//    full 128-byte row segments with non-temporal 16-byte stores.
+//  * Rows past the expert's end are copied from a zero row, so the K loop
+//    has no tail fix-up; a last stage holding <= 16 valid rows runs one
+//    16-row MFMA step instead of two.
+template <int BM, int BN, int WM, int WN, int NST>
+__global__ __launch_bounds__(WM * WN * 64) void wgrad_tile_kernel(WgradArgs a, int num_experts, int per_xcd) {
+  constexpr int NT = WM * WN * 64, BKS = 32;
+  using PTile = MnTile<BM, BKS, NT>;
+  using QTile = MnTile<BN, BKS, NT>;
+  using Mma = MmaTile<BN, BM, WM, WN>;  // transposed: MFMA rows = n2, columns = n1
+  static_assert(Mma::TN == 64 && Mma::TM % 64 == 0, "wave sub-tile is 64 x (64 * HALVES)");
+  constexpr int HALVES = Mma::TM / 64;  // 64-column halves staged one at a time
+  constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
+  constexpr int LPS = PTile::PER_WAVE + QTile::PER_WAVE;
+  constexpr int SUB = 64 * Mma::TN;
+  static_assert(WM * WN * SUB <= NST * STAGE, "staging fits the stage buffers");
+  __shared__ __attribute__((aligned(1024))) bf16 smem[NST * STAGE];
+  const int t2n = a.n2 / BN;
+  const int per_e = (a.n1 / BM) * t2n;
+  const int x = blockIdx.x % kXcds, jb = blockIdx.x / kXcds;
+  const int e = jb / per_xcd;
+  const int t = x * per_xcd + (jb - e * per_xcd);
+  if (e >= num_experts || t >= per_e) return;
+  const int t1 = t / t2n, t2 = t % t2n;
+  const int r0 = min(a.offsets[e], a.rows_cap);
+  const int kr = min(a.offsets[e + 1], a.rows_cap) - r0;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const bf16* pbase = a.p + static_cast<int64_t>(r0) * a.ldp + t1 * BM;
+  const bf16* qbase = a.q + static_cast<int64_t>(r0) * a.ldq + t2 * BN;
+  auto issue = [&](int s) {
+    bf16* dst = smem + (s % NST) * STAGE;
+    const int kb = s * BKS;
+    PTile::issue_rows(dst, [&](int v) {
+      const int k = kb + PTile::k_of(v);
+      return k < kr ? pbase + static_cast<int64_t>(k) * a.ldp : g_wgrad_zero_row;
+    });
+    QTile::issue_rows(dst + PTile::ELEMS, [&](int v) {
+      const int k = kb + QTile::k_of(v);
+      return k < kr ? qbase + static_cast<int64_t>(k) * a.ldq : g_wgrad_zero_row;
+    });
+  };
+  Mma mma;
+  mma.zero();
+  const int nk = (kr + BKS - 1) / BKS;
+  const bool half_tail = (kr & (BKS - 1)) != 0 && (kr & (BKS - 1)) <= 16;  // last stage: one 16-row step
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nk) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+    __syncthreads();  // stage kt landed; stage kt - 1 consumed
+    if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    const bf16* pb = smem + (kt % NST) * STAGE;
+    const int nsub = (kt == nk - 1 && half_tail) ? 1 : 2;
+    for (int ss = 0; ss < nsub; ++ss)
+      mma.template compute<QTile, PTile, 16>(pb + PTile::ELEMS + ss * 16 * BN, pb + ss * 16 * BM, wm, wn, lane);
+  }
+  __syncthreads();  // stage buffers free: each wave stages its sub-tile, 64 columns at a time
+  bf16* stage_out = smem + wave * SUB;
+  bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 +
+              static_cast<int64_t>(t1 * BM + wn * Mma::TN) * a.n2 + t2 * BN + wm * Mma::TM;
+#pragma unroll
+  for (int h = 0; h < HALVES; ++h) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < Mma::NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i = 2 * h + ii;
+          const int r = j * 32 + (lane & 31);
+          const int v = ii * 4 + g;
+          const uint32_t lo = pack_bf16x2(mma.acc[i][j][4 * g], mma.acc[i][j][4 * g + 1]);
+          const uint32_t hi = pack_bf16x2(mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
+          *reinterpret_cast<uint2*>(stage_out + r * 64 + ((v ^ (r & 7)) << 3) + (lane >> 5) * 4) =
+              make_uint2(lo, hi);
+        }
+#pragma unroll
+    for (int it = 0; it < SUB / 8 / 64; ++it) {
+      const int r = it * 8 + (lane >> 3), cv = lane & 7;
+      store_out16(out + static_cast<int64_t>(r) * a.n2 + h * 64 + cv * 8,
+                  *reinterpret_cast<const uint4*>(stage_out + r * 64 + ((cv ^ (r & 7)) << 3)));
+    }
   }
 }
 
@@ -668,6 +780,10 @@ int eight_waves() {
   }
   return v;
 }
+
+enum { WG_WIDE = 0, WG_TILE = 1, WG_LARGE = 2 };
+
+bool wgrad_small_k(int64_t max_rows, int E) { return max_rows <= 128 * static_cast<int64_t>(E); }
 
 template <int BLAYOUT, int EPI>
 int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* ws, hipStream_t s,
@@ -772,32 +888,74 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
   return run_rows<B_NCONTIG, EPI_STORE>(p, offsets, max_rows, num_experts, workspace, s, "mm_grouped_gemm");
 }
 
+extern "C" size_t mm_wgrad_workspace_bytes(int64_t max_rows, int32_t num_experts, int32_t n1, int32_t n2) {
+  if (max_rows <= 0 || num_experts <= 0 || !wgrad_small_k(max_rows, num_experts)) return 0;
+  return mm_align_up(static_cast<size_t>(max_rows) * n1 * 2, 256) + static_cast<size_t>(max_rows) * n2 * 2;
+}
+
 extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows, const uint16_t* q,
                                 int64_t ldq, const int32_t* q_rows, const int32_t* offsets, int32_t num_experts,
                                 int64_t max_rows, int32_t n1, int32_t n2, uint16_t* c, void* workspace,
                                 size_t workspace_bytes, mm_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   MM_CHECK_ARG(p && q && offsets && c, "mm_grouped_wgrad: null pointer");
   MM_CHECK_ARG(num_experts > 0, "mm_grouped_wgrad: bad num_experts");
   MM_CHECK_ARG(n1 > 0 && n1 % 128 == 0 && n2 > 0 && n2 % 128 == 0, "mm_grouped_wgrad: n1, n2 must be multiples of 128");
   MM_CHECK_ARG(ldp % 8 == 0 && ldq % 8 == 0 && al16(p) && al16(q), "mm_grouped_wgrad: 16-byte alignment required");
+  MM_CHECK_ARG(max_rows >= 0 && max_rows < (int64_t(1) << 31), "mm_grouped_wgrad: bad max_rows");
   WgradArgs a{reinterpret_cast<const bf16*>(p), ldp, p_rows, reinterpret_cast<const bf16*>(q), ldq,
-              q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c)};
-  MM_CHECK_ARG(max_rows >= 0, "mm_grouped_wgrad: bad max_rows");
-  // Experts averaging <= 128 rows (K of the wgrad GEMM): small tiles with
-  // direct stores, the output write dominates. Otherwise 256-wide tiles.
-  const bool small_k = max_rows <= 128 * static_cast<int64_t>(num_experts);
-  const int bm = (!small_k && n1 % 256 == 0) ? 256 : 128;
-  const int bn = (!small_k && n2 % 256 == 0) ? 256 : 128;
+              q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c), static_cast<int>(max_rows)};
+  hipStream_t s = mm_hip_stream(stream);
+  // Experts averaging <= 128 rows (K of the wgrad GEMM): the output write
+  // dominates -> 256 x 256 tiles over contiguous operands when n1, n2 allow
+  // and the workspace can hold the permuted copies of gathered operands
+  // (WG_WIDE), else 128 x 128 tiles that gather in place (WG_TILE).
+  // Otherwise 256-wide tiles with a deep K loop (WG_LARGE).
+  // MM_WGRAD_KERNEL=wide|tile|large overrides the choice (wide falls back
+  // to tile where it does not apply).
+  int variant = wgrad_small_k(max_rows, num_experts) ? WG_WIDE : WG_LARGE;
+  if (const char* ev = getenv("MM_WGRAD_KERNEL")) {
+    if (strcmp(ev, "wide") == 0) variant = WG_WIDE;
+    else if (strcmp(ev, "tile") == 0) variant = WG_TILE;
+    else if (strcmp(ev, "large") == 0) variant = WG_LARGE;
+  }
+  if (variant == WG_WIDE) {
+    const size_t pb = p_rows ? mm_align_up(static_cast<size_t>(max_rows) * n1 * 2, 256) : 0;
+    const size_t qb = q_rows ? static_cast<size_t>(max_rows) * n2 * 2 : 0;
+    if (n1 % 256 != 0 || n2 % 256 != 0 || (pb + qb > 0 && (!workspace || workspace_bytes < pb + qb))) {
+      variant = WG_TILE;
+    } else {
+      uint16_t* wsp = static_cast<uint16_t*>(workspace);
+      if (p_rows) {
+        if (int rc = mm_permute(p, ldp, p_rows, offsets, num_experts, max_rows, n1, wsp, n1, stream)) return rc;
+        a.p = reinterpret_cast<const bf16*>(wsp);
+        a.ldp = n1;
+        a.p_rows = nullptr;
+      }
+      if (q_rows) {
+        uint16_t* qd = wsp + pb / 2;
+        if (int rc = mm_permute(q, ldq, q_rows, offsets, num_experts, max_rows, n2, qd, n2, stream)) return rc;
+        a.q = reinterpret_cast<const bf16*>(qd);
+        a.ldq = n2;
+        a.q_rows = nullptr;
+      }
+      const int64_t pe = static_cast<int64_t>(n1 / 256) * (n2 / 256);
+      const int64_t px = (pe + kXcds - 1) / kXcds;
+      const int64_t g = static_cast<int64_t>(num_experts) * px * kXcds;
+      MM_CHECK_ARG(g < (int64_t(1) << 31), "mm_grouped_wgrad: too many tiles");
+      wgrad_tile_kernel<256, 256, 2, 4, 2><<<static_cast<int>(g), 512, 0, s>>>(a, num_experts, static_cast<int>(px));
+      return mm_check_launch("mm_grouped_wgrad");
+    }
+  }
+  const bool small = variant == WG_TILE;
+  const int bm = (!small && n1 % 256 == 0) ? 256 : 128;
+  const int bn = (!small && n2 % 256 == 0) ? 256 : 128;
   const int64_t per_e = static_cast<int64_t>(n1 / bm) * (n2 / bn);
   const int64_t per_xcd = (per_e + kXcds - 1) / kXcds;
   const int64_t grid64 = static_cast<int64_t>(num_experts) * per_xcd * kXcds;
   MM_CHECK_ARG(grid64 < (int64_t(1) << 31), "mm_grouped_wgrad: too many tiles");
   const int grid = static_cast<int>(grid64);
   const int px = static_cast<int>(per_xcd);
-  hipStream_t s = mm_hip_stream(stream);
-  if (small_k) {
+  if (small) {
     grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256 && bn == 256) {
     if (eight_waves())

@@ -60,9 +60,9 @@ __device__ __forceinline__ uint4 f32_to_vec8(const float* f) {
 __global__ __launch_bounds__(kThreads) void permute_kernel(const uint4* __restrict__ x, int64_t ldx_v,
                                                            const int32_t* __restrict__ send_token,
                                                            const int32_t* __restrict__ offsets, int E,
-                                                           int hidden_v, uint4* __restrict__ out,
-                                                           int64_t ldo_v) {
-  const int nvalid = offsets[E];
+                                                           int64_t max_rows, int hidden_v,
+                                                           uint4* __restrict__ out, int64_t ldo_v) {
+  const int nvalid = static_cast<int>(min(static_cast<int64_t>(offsets[E]), max_rows));
   const int lane = threadIdx.x & 63;
   for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
        row += gridDim.x * kRowsPerBlock) {
@@ -197,7 +197,7 @@ extern "C" int mm_permute(const uint16_t* x, int64_t ldx, const int32_t* send_to
                "mm_permute: rows must be 16-byte aligned (hidden, strides multiple of 8)");
   if (max_rows == 0) return MM_OK;
   permute_kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
-      reinterpret_cast<const uint4*>(x), ldx / 8, send_token, offsets, num_experts, hidden / 8,
+      reinterpret_cast<const uint4*>(x), ldx / 8, send_token, offsets, num_experts, max_rows, hidden / 8,
       reinterpret_cast<uint4*>(out), ldo / 8);
   return mm_check_launch("mm_permute");
 }

@@ -32,6 +32,7 @@ SIGNATURES = {
     "mm_route": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "mm_permute": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I64, _I32, _P, _I64, _P]),
     "mm_gemm_workspace_bytes": (_SZ, [_I64, _I32]),
+    "mm_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "mm_fc1_swiglu": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I32, _I32, _I32,
                                      _F32, _F32, _F32, _P, _P, _P, _SZ, _P]),
     "mm_grouped_gemm": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _I32,

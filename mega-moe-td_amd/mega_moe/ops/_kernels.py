@@ -93,9 +93,11 @@ def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int
     if max_rows is None:
         max_rows = q.shape[0] if q_rows is None else q_rows.shape[0]
     c = torch.empty(num_experts, n1, n2, dtype=torch.bfloat16, device=p.device)
+    need = int(_lib.load().mm_wgrad_workspace_bytes(max_rows, num_experts, n1, n2))
+    ws = workspace(p.device, need, "wgrad") if need and (p_rows is not None or q_rows is not None) else None
     _lib.call("mm_grouped_wgrad", _lib.ptr(p), p.stride(0), _lib.ptr(p_rows), _lib.ptr(q), q.stride(0),
-              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), None, 0,
-              _lib.stream_of(p.device))
+              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), _lib.ptr(ws),
+              0 if ws is None else ws.numel(), _lib.stream_of(p.device))
     return c
 
 

@@ -130,18 +130,18 @@ def test_grouped_gemm(layout, kind, gather):
 
 @pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
 @pytest.mark.parametrize("gather", [False, True])
-@pytest.mark.parametrize("tiling", ["small_k", "large_k"])
-def test_grouped_wgrad(kind, gather, tiling):
+@pytest.mark.parametrize("tiling", ["wide", "tile", "large"])
+def test_grouped_wgrad(kind, gather, tiling, monkeypatch):
     from mega_moe.ops import _kernels as K
-    E, N1, N2 = 5, 256, 128
+    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling)  # the kernel variant; read on every call
+    E, N1, N2 = 5, 256, 256
     offs = _ragged(E, kind, seed=4)
     M = int(offs[-1])
     g = torch.Generator(device=DEV).manual_seed(1)
     p = torch.randn(M + 9, N1, device=DEV, generator=g).to(torch.bfloat16)
     q = torch.randn(M, N2, device=DEV, generator=g).to(torch.bfloat16)
     p_rows = torch.randint(0, M + 9, (M,), device=DEV, dtype=torch.int32, generator=g) if gather else None
-    # max_rows only selects the tiling: 0 forces the small-K variant
-    c = K.grouped_wgrad(p, p_rows, q, None, offs, N1, N2, max_rows=0 if tiling == "small_k" else 1 << 20)
+    c = K.grouped_wgrad(p, p_rows, q, None, offs, N1, N2, max_rows=M)
     torch.cuda.synchronize()
     pf = p.float().cpu()
     pf = pf[p_rows.long().cpu()] if gather else pf[:M]
@@ -154,6 +154,37 @@ def test_grouped_wgrad(kind, gather, tiling):
     for e in range(E):
         if o[e + 1] == o[e]:
             assert torch.count_nonzero(c[e]) == 0
+
+
+@pytest.mark.parametrize("tiling", ["wide", "tile"])
+def test_grouped_wgrad_many_experts_both_gathered(tiling, monkeypatch):
+    """Small-K regime with many experts: rows 0..140 per expert (zero-row
+    experts, a last K stage of <= 16 rows, multi-stage K, one 300-row
+    expert), both operands gathered (permuted into the workspace first)."""
+    from mega_moe.ops import _kernels as K
+    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling)
+    E, N1, N2 = 21, 512, 1280
+    rng = np.random.default_rng(11)
+    cnt = rng.integers(0, 141, size=E)
+    cnt[[2, 9]] = 0
+    cnt[5] = 300
+    offs = torch.from_numpy(np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)).to(DEV)
+    M = int(offs[-1])
+    g = torch.Generator(device=DEV).manual_seed(2)
+    p = torch.randn(M + 3, N1, device=DEV, generator=g).to(torch.bfloat16)
+    q = torch.randn(M + 5, N2, device=DEV, generator=g).to(torch.bfloat16)
+    p_rows = torch.randint(0, M + 3, (M,), device=DEV, dtype=torch.int32, generator=g)
+    q_rows = torch.randperm(M + 5, device=DEV, generator=g)[:M].to(torch.int32)
+    c = K.grouped_wgrad(p, p_rows, q, q_rows, offs, N1, N2, max_rows=M)
+    torch.cuda.synchronize()
+    pf = p.float().cpu()[p_rows.long().cpu()]
+    qf = q.float().cpu()[q_rows.long().cpu()]
+    o = offs.cpu().tolist()
+    ref = torch.zeros(E, N1, N2)
+    for e in range(E):
+        ref[e] = pf[o[e]:o[e + 1]].T @ qf[o[e]:o[e + 1]]
+    assert_rel(c, ref, 1e-2, "grouped_wgrad")
+    assert torch.count_nonzero(c[2]) == 0 and torch.count_nonzero(c[9]) == 0
 
 
 def test_combine_integer_exact():
