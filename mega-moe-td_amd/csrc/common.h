@@ -54,7 +54,9 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f
 // ---------------------------------------------------------------- activation
 // Gated activation value act(gate) * v(up) in fp32, following the reference's
 // _gated_activation (ops/_torch_forward.py:177-205).
-__device__ __forceinline__ float mm_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// v_exp_f32 and v_rcp_f32 (about 1 ulp each; the results are rounded to
+// bf16 afterwards).
+__device__ __forceinline__ float mm_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 __device__ __forceinline__ float mm_tanh(float x) {
   // tanh(x) = 2*sigmoid(2x) - 1 (same rewrite the reference kernels use).

@@ -48,12 +48,8 @@ __device__ __forceinline__ void vec8_to_f32(const uint4& v, float* f) {
 }
 
 __device__ __forceinline__ uint4 f32_to_vec8(const float* f) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    w[i] = static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i])) |
-           (static_cast<uint32_t>(f32_to_bf16_bits(f[2 * i + 1])) << 16);
-  return make_uint4(w[0], w[1], w[2], w[3]);
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
 }
 
 // out[i] = x[send_token[i]] for i < offsets[E].
@@ -73,6 +69,10 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const uint4* __restri
 }
 
 // out[t] = bf16(sum_j fp32(y[route_to_send[t*k+j]])), slot order j = 0..k-1.
+// A wavefront owns one token row; each lane handles VPL 16-byte vectors of
+// the row per pass and issues the loads of 4 slots for all of them before
+// accumulating, so 4 * VPL row reads are in flight per lane.
+template <int VPL>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restrict__ y, int64_t ldy_v,
                                                            const int32_t* __restrict__ route_to_send,
                                                            int64_t T, int top_k, int hidden_v,
@@ -82,18 +82,42 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restri
        t += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
     const int my_row = lane < top_k ? route_to_send[t * top_k + lane] : -1;
     uint4* dst = out + t * ldo_v;
-    for (int v = lane; v < hidden_v; v += 64) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int j = 0; j < top_k; ++j) {
-        const int r = __shfl(my_row, j);
-        if (r >= 0) {
-          float f[8];
-          vec8_to_f32(y[static_cast<int64_t>(r) * ldy_v + v], f);
+    for (int v0 = lane; v0 < hidden_v; v0 += 64 * VPL) {
+      float acc[VPL][8];
 #pragma unroll
-          for (int q = 0; q < 8; ++q) acc[q] += f[q];
+      for (int u = 0; u < VPL; ++u)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[u][q] = 0.0f;
+      for (int j0 = 0; j0 < top_k; j0 += 4) {
+        uint4 val[4][VPL];
+        int rr[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = j0 + jj;
+          rr[jj] = __shfl(my_row, j < top_k ? j : 0);
+          if (j >= top_k) rr[jj] = -1;
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            const int v = v0 + u * 64;
+            val[jj][u] = (rr[jj] >= 0 && v < hidden_v) ? y[static_cast<int64_t>(rr[jj]) * ldy_v + v]
+                                                        : make_uint4(0, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          if (rr[jj] < 0) continue;
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) {
+            float f[8];
+            vec8_to_f32(val[jj][u], f);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[u][q] += f[q];
+          }
         }
       }
-      dst[v] = f32_to_vec8(acc);
+#pragma unroll
+      for (int u = 0; u < VPL; ++u)
+        if (v0 + u * 64 < hidden_v) dst[v0 + u * 64] = f32_to_vec8(acc[u]);
     }
   }
 }
@@ -142,10 +166,12 @@ __device__ __forceinline__ void act_pair(int kind, float a, float b, float beta,
   }
 }
 
+template <int KIND>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
     const uint4* __restrict__ ga, int64_t ld_ga_v, const uint4* __restrict__ fc1, int64_t ld_fc1_v,
-    const float* __restrict__ scale, const int32_t* __restrict__ offsets, int E, int inter_v, int kind,
+    const float* __restrict__ scale, const int32_t* __restrict__ offsets, int E, int inter_v,
     float beta, float lbeta, float L, uint4* __restrict__ dab, uint16_t* __restrict__ dscale) {
+  constexpr int kind = KIND;
   const int nvalid = offsets[E];
   const int lane = threadIdx.x & 63;
   for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
@@ -155,21 +181,36 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
     const uint4* a_row = fc1 + static_cast<int64_t>(row) * ld_fc1_v;
     uint4* d_row = dab + static_cast<int64_t>(row) * ld_fc1_v;
     float part = 0.0f;
-    for (int v = lane; v < inter_v; v += 64) {
-      float dc[8], a[8], b[8], da[8], db[8];
-      vec8_to_f32(g_row[v], dc);
-      vec8_to_f32(a_row[v], a);
-      vec8_to_f32(a_row[inter_v + v], b);
+    // two 16-byte vectors per lane per pass: all six loads issue before the math
+    for (int v0 = lane; v0 < inter_v; v0 += 128) {
+      uint4 gv[2], av[2], bv[2];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float act_a, dact_a, vv, dv;
-        act_pair(kind, a[q], b[q], beta, lbeta, L, act_a, dact_a, vv, dv);
-        da[q] = dc[q] * dact_a * vv * s;
-        db[q] = dc[q] * act_a * dv * s;
-        part += act_a * vv * dc[q];
+      for (int u = 0; u < 2; ++u) {
+        const int v = v0 + 64 * u;
+        const bool in = v < inter_v;
+        gv[u] = in ? g_row[v] : make_uint4(0, 0, 0, 0);
+        av[u] = in ? a_row[v] : make_uint4(0, 0, 0, 0);
+        bv[u] = in ? a_row[inter_v + v] : make_uint4(0, 0, 0, 0);
       }
-      d_row[v] = f32_to_vec8(da);
-      d_row[inter_v + v] = f32_to_vec8(db);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int v = v0 + 64 * u;
+        if (v >= inter_v) break;
+        float dc[8], a[8], b[8], da[8], db[8];
+        vec8_to_f32(gv[u], dc);
+        vec8_to_f32(av[u], a);
+        vec8_to_f32(bv[u], b);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          float act_a, dact_a, vv, dv;
+          act_pair(kind, a[q], b[q], beta, lbeta, L, act_a, dact_a, vv, dv);
+          da[q] = dc[q] * dact_a * vv * s;
+          db[q] = dc[q] * act_a * dv * s;
+          part += act_a * vv * dc[q];
+        }
+        d_row[v] = f32_to_vec8(da);
+        d_row[inter_v + v] = f32_to_vec8(db);
+      }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
@@ -210,7 +251,7 @@ extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_t
   MM_CHECK_ARG(y && route_to_send && out, "mm_combine: null pointer");
   MM_CHECK_ARG(hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) && aligned16(out),
                "mm_combine: rows must be 16-byte aligned");
-  combine_kernel<<<grid_for_rows(num_tokens), kThreads, 0, mm_hip_stream(stream)>>>(
+  combine_kernel<2><<<grid_for_rows(num_tokens), kThreads, 0, mm_hip_stream(stream)>>>(
       reinterpret_cast<const uint4*>(y), ldy / 8, route_to_send, num_tokens, top_k, hidden / 8,
       reinterpret_cast<uint4*>(out), ldo / 8);
   return mm_check_launch("mm_combine");
@@ -239,9 +280,17 @@ extern "C" int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga, const uint
   MM_CHECK_ARG(aligned16(grad_act) && aligned16(fc1_out) && aligned16(dab), "mm_swiglu_bwd: misaligned");
   MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_swiglu_bwd: bad act_kind");
   if (max_rows == 0) return MM_OK;
-  swiglu_bwd_kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
-      reinterpret_cast<const uint4*>(grad_act), ld_ga / 8, reinterpret_cast<const uint4*>(fc1_out), ld_fc1 / 8,
-      scale, offsets, num_experts, inter / 8, act_kind, situ_beta, situ_linear_beta, clamp_limit,
-      reinterpret_cast<uint4*>(dab), dscale);
+  auto launch = [&](auto kernel) {
+    kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
+        reinterpret_cast<const uint4*>(grad_act), ld_ga / 8, reinterpret_cast<const uint4*>(fc1_out),
+        ld_fc1 / 8, scale, offsets, num_experts, inter / 8, situ_beta, situ_linear_beta, clamp_limit,
+        reinterpret_cast<uint4*>(dab), dscale);
+  };
+  if (act_kind == MM_ACT_SWIGLU)
+    launch(swiglu_bwd_kernel<MM_ACT_SWIGLU>);
+  else if (act_kind == MM_ACT_CLAMP_SWIGLU)
+    launch(swiglu_bwd_kernel<MM_ACT_CLAMP_SWIGLU>);
+  else
+    launch(swiglu_bwd_kernel<MM_ACT_SITUGLU>);
   return mm_check_launch("mm_swiglu_bwd");
 }
