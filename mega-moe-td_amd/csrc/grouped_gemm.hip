@@ -413,15 +413,27 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   Mma mma;
   mma.zero();
   const int nk = p.k / BK_;
+  // waves whose row slab lies entirely past the tile's valid rows (the
+  // partial last tile of an expert) skip their MFMAs; their accumulators stay
+  // zero and those rows are never stored
+  const bool active = wm * Mma::TM < rows;
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s)
     if (s < nk) issue(s);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
-    __syncthreads();
-    if (kt + NST - 1 < nk) issue(kt + NST - 1);
-    const bf16* cur = smem + (kt % NST) * STAGE;
-    mma.template compute<ATile, BTile, BK_>(cur, cur + ATile::ELEMS, wm, wn, lane);
+  if (active) {
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+      __syncthreads();
+      if (kt + NST - 1 < nk) issue(kt + NST - 1);
+      const bf16* cur = smem + (kt % NST) * STAGE;
+      mma.template compute<ATile, BTile, BK_>(cur, cur + ATile::ELEMS, wm, wn, lane);
+    }
+  } else {  // same copies and barriers, no MFMAs
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
+      __syncthreads();
+      if (kt + NST - 1 < nk) issue(kt + NST - 1);
+    }
   }
   __syncthreads();
 
