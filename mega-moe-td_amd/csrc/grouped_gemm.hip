@@ -781,9 +781,11 @@ void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) 
   grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT><<<grid, NT, 0, s>>>(p);
 }
 
-// 8 waves (2 per SIMD) per 256-row workgroup by default: a second wave on
-// each SIMD keeps the matrix core busy across the other's LDS waits and
-// barriers (measured +10% over 4 waves). MM_GEMM_WAVES=4 selects 4 waves.
+// 8 waves (2 per SIMD) per 256x256 and 128x256 workgroup by default: a
+// second wave on each SIMD keeps the matrix core busy across the other's
+// LDS waits and barriers (measured +10% over 4 waves on 256-row tiles, -7%
+// time on the 128-row tiles of small experts). MM_GEMM_WAVES=4 selects 4
+// waves.
 int eight_waves() {
   static int v = -1;
   if (v < 0) {
@@ -811,7 +813,7 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     else
       launch_rows_cfg<256, 256, 32, 4, BLAYOUT, EPI>(p, max_rows, E, s);
   } else if (c.bn == 256) {
-    if (eight_waves() && getenv("MM_GEMM_MED8"))
+    if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
       launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
     else
       launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
