@@ -640,97 +640,184 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
 // output write dominates.
 __device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
 
-// One BM x BN output tile per workgroup over contiguous operands (gathered
-// operands are permuted into the workspace first by the host side).
+// wait until at most n (rounded down to a multiple of STEP) vector-memory
+// ops of this wave are outstanding; n is wave-uniform
+template <int MAXN, int STEP>
+__device__ __forceinline__ void wait_vmcnt_atmost(int n) {
+  if constexpr (MAXN > 0) {
+    if (n >= MAXN) {
+      wait_vmcnt<MAXN>();
+      return;
+    }
+    wait_vmcnt_atmost<MAXN - STEP, STEP>(n);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// Small-K weight gradient over contiguous operands (gathered operands are
+// permuted into the workspace first by the host side).
+//  * Persistent: one 8-wave workgroup per CU walks a sequence of (expert,
+//    256 x 256 output tile, 32-row K step) stages through an NST-deep LDS
+//    ring, so the first stages of the next tile are in flight while the
+//    current tile is staged and stored. XCD x (workgroup ids congruent to x
+//    mod 8) owns experts x, x + 8, ...: every expert writes the same n1 x n2
+//    output whatever its row count, so this is balanced, and an expert's
+//    rows are read into that XCD's L2 once. The workgroups of an XCD take
+//    every (gridDim / 8)-th tile of each expert.
 //  * The product is formed transposed, C^T = Q^T P, so each lane's
-//    accumulator holds 4 consecutive output columns of one output row: every
-//    wave stages its sub-tile 64 columns at a time in its own slice of the
-//    (then idle) stage buffers with 8-byte LDS writes and writes it back as
-//    full 128-byte row segments with non-temporal 16-byte stores.
+//    accumulator holds 4 consecutive output columns of one output row; every
+//    wave stages its 64 x 128 sub-tile 64 columns at a time in a private LDS
+//    slice with 8-byte writes and writes it back as full 128-byte row
+//    segments with non-temporal 16-byte stores. The staging is separate from
+//    the ring and wave-private, so tiles need no barrier of their own.
 //  * Rows past the expert's end are copied from a zero row, so the K loop
-//    has no tail fix-up; a last stage holding <= 16 valid rows runs one
-//    16-row MFMA step instead of two.
-template <int BM, int BN, int WM, int WN, int NST>
-__global__ __launch_bounds__(WM * WN * 64) void wgrad_tile_kernel(WgradArgs a, int num_experts, int per_xcd) {
-  constexpr int NT = WM * WN * 64, BKS = 32;
+//    has no tail fix-up; a stage holding <= 16 valid rows runs one 16-row
+//    MFMA step instead of two.
+//  * Every wave issues the same vector-memory ops (LPS copies per stage, SPT
+//    stores per tile), and they complete in issue order, so each stage wait
+//    counts exactly the ops issued after that stage.
+struct TileCursor {
+  int e, t, ks, nk, kr, r0;
+  bool valid;
+  __device__ void load_expert(const int32_t* offsets, int rows_cap) {
+    r0 = __builtin_amdgcn_readfirstlane(min(offsets[e], rows_cap));
+    kr = __builtin_amdgcn_readfirstlane(min(offsets[e + 1], rows_cap)) - r0;
+    nk = kr > 0 ? (kr + 31) / 32 : 1;  // an expert without rows still writes its zero tiles
+  }
+  __device__ void skip_empty(int c, int per_e, int E, const int32_t* offsets, int rows_cap) {
+    while (valid && t >= per_e) {
+      e += kXcds;
+      t = c;
+      valid = e < E;
+    }
+    if (valid) load_expert(offsets, rows_cap);
+  }
+  __device__ void init(int x, int c, int per_e, int E, const int32_t* offsets, int rows_cap) {
+    e = x;
+    t = c;
+    ks = 0;
+    valid = e < E;
+    skip_empty(c, per_e, E, offsets, rows_cap);
+  }
+  __device__ void advance(int c, int nc, int per_e, int E, const int32_t* offsets, int rows_cap) {
+    if (++ks < nk) return;
+    ks = 0;
+    t += nc;
+    if (t >= per_e) skip_empty(c, per_e, E, offsets, rows_cap);
+  }
+};
+
+template <int NST>
+__global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num_experts) {
+  constexpr int BM = 256, BN = 256, BKS = 32, WM = 2, WN = 4, NT = WM * WN * 64;
   using PTile = MnTile<BM, BKS, NT>;
   using QTile = MnTile<BN, BKS, NT>;
   using Mma = MmaTile<BN, BM, WM, WN>;  // transposed: MFMA rows = n2, columns = n1
-  static_assert(Mma::TN == 64 && Mma::TM % 64 == 0, "wave sub-tile is 64 x (64 * HALVES)");
-  constexpr int HALVES = Mma::TM / 64;  // 64-column halves staged one at a time
+  static_assert(Mma::TN == 64 && Mma::TM == 128, "wave sub-tile is 64 x 128");
+  constexpr int HALVES = Mma::TM / 64;
   constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
-  constexpr int LPS = PTile::PER_WAVE + QTile::PER_WAVE;
-  constexpr int SUB = 64 * Mma::TN;
-  static_assert(WM * WN * SUB <= NST * STAGE, "staging fits the stage buffers");
-  __shared__ __attribute__((aligned(1024))) bf16 smem[NST * STAGE];
+  constexpr int LPS = PTile::PER_WAVE + QTile::PER_WAVE;  // copies per wave per stage
+  constexpr int SUB = 64 * Mma::TN;                       // staging elements per wave
+  constexpr int SPT = HALVES * SUB / 8 / 64;              // stores per lane per tile
+  __shared__ __attribute__((aligned(1024))) bf16 smem[NST * STAGE + (NT / 64) * SUB];
+  const int x = blockIdx.x % kXcds, c = blockIdx.x / kXcds, nc = gridDim.x / kXcds;
   const int t2n = a.n2 / BN;
   const int per_e = (a.n1 / BM) * t2n;
-  const int x = blockIdx.x % kXcds, jb = blockIdx.x / kXcds;
-  const int e = jb / per_xcd;
-  const int t = x * per_xcd + (jb - e * per_xcd);
-  if (e >= num_experts || t >= per_e) return;
-  const int t1 = t / t2n, t2 = t % t2n;
-  const int r0 = min(a.offsets[e], a.rows_cap);
-  const int kr = min(a.offsets[e + 1], a.rows_cap) - r0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const bf16* pbase = a.p + static_cast<int64_t>(r0) * a.ldp + t1 * BM;
-  const bf16* qbase = a.q + static_cast<int64_t>(r0) * a.ldq + t2 * BN;
-  auto issue = [&](int s) {
-    bf16* dst = smem + (s % NST) * STAGE;
-    const int kb = s * BKS;
+  bf16* stage_out = smem + NST * STAGE + wave * SUB;
+
+  TileCursor cc, lc;  // consumer; copier (NST - 1 stages ahead)
+  cc.init(x, c, per_e, num_experts, a.offsets, a.rows_cap);
+  lc = cc;
+  auto issue = [&](const TileCursor& q, int buf) {
+    bf16* dst = smem + buf * STAGE;
+    const int t1 = q.t / t2n, t2 = q.t % t2n;
+    const int kb = q.ks * BKS;
+    const bf16* prow0 = a.p + static_cast<int64_t>(q.r0 + kb) * a.ldp + t1 * BM;
+    const bf16* qrow0 = a.q + static_cast<int64_t>(q.r0 + kb) * a.ldq + t2 * BN;
+    const int kv = q.kr - kb;
     PTile::issue_rows(dst, [&](int v) {
-      const int k = kb + PTile::k_of(v);
-      return k < kr ? pbase + static_cast<int64_t>(k) * a.ldp : g_wgrad_zero_row;
+      const int k = PTile::k_of(v);
+      return k < kv ? prow0 + static_cast<int64_t>(k) * a.ldp : g_wgrad_zero_row;
     });
     QTile::issue_rows(dst + PTile::ELEMS, [&](int v) {
-      const int k = kb + QTile::k_of(v);
-      return k < kr ? qbase + static_cast<int64_t>(k) * a.ldq : g_wgrad_zero_row;
+      const int k = QTile::k_of(v);
+      return k < kv ? qrow0 + static_cast<int64_t>(k) * a.ldq : g_wgrad_zero_row;
     });
   };
+
+  // vector-memory ops issued by this wave so far, and the count right after
+  // each in-flight stage's copies (ring slot st % NST)
+  int issued_ops = 0;
+  int stage_mark[NST];
+#pragma unroll
+  for (int i = 0; i < NST; ++i) stage_mark[i] = 0;
+  int nissued = 0;
+  for (; nissued < NST - 1 && lc.valid; ++nissued) {
+    issue(lc, nissued % NST);
+    issued_ops += LPS;
+#pragma unroll
+    for (int i = 0; i < NST; ++i)
+      if (i == nissued % NST) stage_mark[i] = issued_ops;
+    lc.advance(c, nc, per_e, num_experts, a.offsets, a.rows_cap);
+  }
   Mma mma;
   mma.zero();
-  const int nk = (kr + BKS - 1) / BKS;
-  const bool half_tail = (kr & (BKS - 1)) != 0 && (kr & (BKS - 1)) <= 16;  // last stage: one 16-row step
+  for (int st = 0; cc.valid; ++st) {
+    int mark = 0;
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
-    if (s < nk) issue(s);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_stages<LPS, NST - 2>(min(nk - 1, kt + NST - 2) - kt);
-    __syncthreads();  // stage kt landed; stage kt - 1 consumed
-    if (kt + NST - 1 < nk) issue(kt + NST - 1);
-    const bf16* pb = smem + (kt % NST) * STAGE;
-    const int nsub = (kt == nk - 1 && half_tail) ? 1 : 2;
+    for (int i = 0; i < NST; ++i)
+      if (i == st % NST) mark = stage_mark[i];
+    wait_vmcnt_atmost<(NST - 2) * LPS + (NST - 1) * SPT, 4>(issued_ops - mark);
+    __syncthreads();  // stage st landed; stage st - 1 consumed by every wave
+    if (lc.valid) {
+      issue(lc, nissued % NST);
+      issued_ops += LPS;
+#pragma unroll
+      for (int i = 0; i < NST; ++i)
+        if (i == nissued % NST) stage_mark[i] = issued_ops;
+      lc.advance(c, nc, per_e, num_experts, a.offsets, a.rows_cap);
+      ++nissued;
+    }
+    const bf16* pb = smem + (st % NST) * STAGE;
+    const int kv = cc.kr - cc.ks * BKS;
+    const int nsub = kv > 16 ? 2 : 1;  // a stage with <= 16 valid rows runs one 16-row step
     for (int ss = 0; ss < nsub; ++ss)
       mma.template compute<QTile, PTile, 16>(pb + PTile::ELEMS + ss * 16 * BN, pb + ss * 16 * BM, wm, wn, lane);
-  }
-  __syncthreads();  // stage buffers free: each wave stages its sub-tile, 64 columns at a time
-  bf16* stage_out = smem + wave * SUB;
-  bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 +
-              static_cast<int64_t>(t1 * BM + wn * Mma::TN) * a.n2 + t2 * BN + wm * Mma::TM;
+    if (cc.ks == cc.nk - 1) {
+      const int t1 = cc.t / t2n, t2 = cc.t % t2n;
+      bf16* out = a.c + static_cast<int64_t>(cc.e) * a.n1 * a.n2 +
+                  static_cast<int64_t>(t1 * BM + wn * Mma::TN) * a.n2 + t2 * BN + wm * Mma::TM;
 #pragma unroll
-  for (int h = 0; h < HALVES; ++h) {
+      for (int h = 0; h < HALVES; ++h) {
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int j = 0; j < Mma::NI; ++j)
+          for (int j = 0; j < Mma::NI; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int i = 2 * h + ii;
-          const int r = j * 32 + (lane & 31);
-          const int v = ii * 4 + g;
-          const uint32_t lo = pack_bf16x2(mma.acc[i][j][4 * g], mma.acc[i][j][4 * g + 1]);
-          const uint32_t hi = pack_bf16x2(mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
-          *reinterpret_cast<uint2*>(stage_out + r * 64 + ((v ^ (r & 7)) << 3) + (lane >> 5) * 4) =
-              make_uint2(lo, hi);
+            for (int g = 0; g < 4; ++g) {
+              const int i = 2 * h + ii;
+              const int r = j * 32 + (lane & 31);
+              const int v = ii * 4 + g;
+              const uint32_t lo = pack_bf16x2(mma.acc[i][j][4 * g], mma.acc[i][j][4 * g + 1]);
+              const uint32_t hi = pack_bf16x2(mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
+              *reinterpret_cast<uint2*>(stage_out + r * 64 + ((v ^ (r & 7)) << 3) + (lane >> 5) * 4) =
+                  make_uint2(lo, hi);
+            }
+#pragma unroll
+        for (int it = 0; it < SUB / 8 / 64; ++it) {
+          const int r = it * 8 + (lane >> 3), cv = lane & 7;
+          store_out16(out + static_cast<int64_t>(r) * a.n2 + h * 64 + cv * 8,
+                      *reinterpret_cast<const uint4*>(stage_out + r * 64 + ((cv ^ (r & 7)) << 3)));
         }
-#pragma unroll
-    for (int it = 0; it < SUB / 8 / 64; ++it) {
-      const int r = it * 8 + (lane >> 3), cv = lane & 7;
-      store_out16(out + static_cast<int64_t>(r) * a.n2 + h * 64 + cv * 8,
-                  *reinterpret_cast<const uint4*>(stage_out + r * 64 + ((cv ^ (r & 7)) << 3)));
+      }
+      issued_ops += SPT;
+      mma.zero();
     }
+    cc.advance(c, nc, per_e, num_experts, a.offsets, a.rows_cap);
   }
 }
 
@@ -796,6 +883,21 @@ int eight_waves() {
 }
 
 enum { WG_WIDE = 0, WG_TILE = 1, WG_LARGE = 2 };
+
+constexpr int kWideStages = 3;  // LDS: 3 x 32 KiB ring + 64 KiB staging = 160 KiB
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
 bool wgrad_small_k(int64_t max_rows, int E) { return max_rows <= 128 * static_cast<int64_t>(E); }
 
@@ -952,11 +1054,8 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
         a.ldq = n2;
         a.q_rows = nullptr;
       }
-      const int64_t pe = static_cast<int64_t>(n1 / 256) * (n2 / 256);
-      const int64_t px = (pe + kXcds - 1) / kXcds;
-      const int64_t g = static_cast<int64_t>(num_experts) * px * kXcds;
-      MM_CHECK_ARG(g < (int64_t(1) << 31), "mm_grouped_wgrad: too many tiles");
-      wgrad_tile_kernel<256, 256, 2, 4, 2><<<static_cast<int>(g), 512, 0, s>>>(a, num_experts, static_cast<int>(px));
+      const int g = device_cus() / kXcds * kXcds;
+      wgrad_persist_kernel<kWideStages><<<g > 0 ? g : kXcds, 512, 0, s>>>(a, num_experts);
       return mm_check_launch("mm_grouped_wgrad");
     }
   }
