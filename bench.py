@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="e32")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--save-fc1-dtype", default="bf16", choices=("bf16", "fp16", "fp8"),
+                    help="saved FC1 format of the training configs (MoEForwardConfig.save_fc1_dtype)")
     ap.add_argument("--cpu-tokens", type=int, default=0, help="token sample for the CPU baseline (0 = auto)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -134,7 +136,8 @@ def main():
           f"k={spec.top_k} backward={spec.backward}", file=sys.stderr, flush=True)
     inp = make_inputs(spec, device=dev, seed=1234)
     op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=spec.tokens, hidden_size=spec.hidden,
-                                  top_k=spec.top_k, num_experts=spec.experts)
+                                  top_k=spec.top_k, num_experts=spec.experts,
+                                  config=mega_moe.MoEForwardConfig(save_fc1_dtype=args.save_fc1_dtype))
 
     def step():
         if spec.backward:
@@ -206,7 +209,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, config routing)",
         "config": {"workload": f"{spec.name}: T={spec.tokens} H={spec.hidden} I={spec.inter} E={spec.experts} "
-                               f"top-{spec.top_k} {'fwd+bwd' if spec.backward else 'fwd'}",
+                               f"top-{spec.top_k} {'fwd+bwd' if spec.backward else 'fwd'}"
+                               + (f" save_fc1={args.save_fc1_dtype}" if spec.backward and args.save_fc1_dtype != "bf16"
+                                  else ""),
                    "global_batch": spec.tokens, "parallelism": "single GPU, all experts resident"},
         "stages_ms": stages,
         "roofline": roof,

@@ -37,6 +37,23 @@ typedef struct ihipStream_t* mm_stream_t; /* == hipStream_t */
 #define MM_ACT_SITUGLU 1
 #define MM_ACT_CLAMP_SWIGLU 2
 
+/*
+ * Formats of the saved raw FC1 output (MoEForwardConfig.save_fc1_dtype,
+ * src/mega_moe/config.py:178-186; src/mega_moe/ops/forward.py:625-651):
+ *   BF16  the raw gate/up values.
+ *   FP16  the same bf16 values stored as fp16 (exact within fp16 range).
+ *   FP8   E4M3 (OCP "fn": max 448) of value * 448 / amax, with one fp32
+ *         scale amax / 448 per row and per MM_FC1_SCALE_GROUP-column group
+ *         (amax over the group's |bf16 values|, 1 for an all-zero group);
+ *         scale table [rows, 2I / MM_FC1_SCALE_GROUP], gate groups then up
+ *         groups; dequantized value = e4m3 * scale
+ *         (kernels/fused_forward.py:893-942, kernels/mega_bwd.py:3185-3206).
+ */
+#define MM_FC1_BF16 0
+#define MM_FC1_FP16 1
+#define MM_FC1_FP8 2
+#define MM_FC1_SCALE_GROUP 128
+
 const char* mm_last_error(void);
 int mm_version(void);
 
@@ -97,14 +114,17 @@ size_t mm_gemm_workspace_bytes(int64_t max_rows, int32_t num_experts);
  *   act[i, j]  = bf16(act_fn(gate, up) * weight_perm[i])
  * row(i) = send_token[i] when send_token != NULL (fused dispatch gather),
  * else i. w1 is [E, H, 2I] contiguous (gate_up_weight). fc1_out
- * ([rows, 2I] = [gate | up] bf16) may be NULL.
+ * ([rows, 2I] = [gate | up] in fc1_format, row stride 2I elements) may be
+ * NULL; MM_FC1_FP8 needs I % MM_FC1_SCALE_GROUP == 0 and fc1_scale
+ * ([rows, 2I / MM_FC1_SCALE_GROUP] fp32), which is ignored otherwise.
  */
 int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send_token,
                   const uint16_t* w1, const int32_t* offsets,
                   const float* weight_perm, int32_t num_experts,
                   int64_t max_rows, int32_t hidden, int32_t inter,
                   int32_t act_kind, float situ_beta, float situ_linear_beta,
-                  float clamp_limit, uint16_t* act, uint16_t* fc1_out,
+                  float clamp_limit, uint16_t* act, void* fc1_out,
+                  int32_t fc1_format, float* fc1_scale,
                   void* workspace, size_t workspace_bytes, mm_stream_t stream);
 
 /*
@@ -174,7 +194,8 @@ int mm_gather_route_grad(const uint16_t* dscale, const int32_t* route_to_send,
 
 /*
  * Gated-activation backward per expert-major row i < offsets[E]:
- *   a = gate, b = up (from fc1_out [rows, 2I] bf16), dc = grad_act [rows, I],
+ *   a = gate, b = up (from fc1_out [rows, 2I] in fc1_format, dequantized
+ *       with fc1_scale for MM_FC1_FP8), dc = grad_act [rows, I],
  *   s = bf16(scale[i]) (the routing weight rounded to bf16, as the reference's
  *       saved recv_weights_sorted is; ops/_torch_forward.py:267)
  *   dAB[i] = bf16([dc*act'(a)*v(b)*s | dc*act(a)*v'(b)*s]),
@@ -182,7 +203,8 @@ int mm_gather_route_grad(const uint16_t* dscale, const int32_t* route_to_send,
  * Replaces kernel_swiglu_bwd (kernels/swiglu_bwd.py:15-83).
  */
 int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga,
-                  const uint16_t* fc1_out, int64_t ld_fc1, const float* scale,
+                  const void* fc1_out, int64_t ld_fc1, int32_t fc1_format,
+                  const float* fc1_scale, const float* scale,
                   const int32_t* offsets, int32_t num_experts,
                   int64_t max_rows, int32_t inter, int32_t act_kind,
                   float situ_beta, float situ_linear_beta, float clamp_limit,

@@ -41,6 +41,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// Two fp32 -> packed fp16 (v_cvt_pk_f16_f32 / RNE).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
@@ -50,6 +57,40 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---------------------------------------------------------------- saved FC1 formats
+// FP8 E4M3 ("fn": bias 7, no infinities, max 448, NaN = 0x7F/0xFF) with
+// round-to-nearest-even and saturation to +-448, the conversion the
+// reference's single-kernel save applies (kernels/fused_forward.py:893-942).
+constexpr float kFp8Max = 448.0f;
+
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;        // NaN
+  if (a > 0x43e80000u) return sign | 0x7eu;        // beyond the 448/480 midpoint: saturate
+  if (a < 0x3c800000u) {                           // below 2^-6: subnormal steps of 2^-9
+    const float m = __builtin_rintf(__uint_as_float(a) * 512.0f);  // RNE, 0..8 (8 = smallest normal)
+    return sign | static_cast<uint32_t>(m);
+  }
+  // normal: round the 23-bit mantissa to 3 bits (RNE, carries into the
+  // exponent), then rebias the exponent from 127 to 7
+  const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
+  return sign | (r - (120u << 3));
+}
+
+__device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+  float v;
+  if (e == 0)
+    v = static_cast<float>(m) * (1.0f / 512.0f);
+  else if (e == 15 && m == 7)
+    v = __uint_as_float(0x7fc00000u);
+  else
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -v : v;
+}
 
 // ---------------------------------------------------------------- activation
 // Gated activation value act(gate) * v(up) in fp32, following the reference's

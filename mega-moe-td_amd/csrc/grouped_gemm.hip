@@ -340,7 +340,9 @@ struct RowsArgs {
   const TileList* tl;
   // gated (FC1) epilogue
   const float* w;
-  bf16* fc1_out;
+  void* fc1_out;   // saved raw gate | up in fc1_fmt (MM_FC1_*), or null
+  int fc1_fmt;
+  float* fc1_scale;  // FP8 scale table [rows, 2I / MM_FC1_SCALE_GROUP]
   int inter;
   int act_kind;
   float beta, lbeta, clamp;
@@ -465,28 +467,86 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
     __syncthreads();
     constexpr int VPR = BN / 16;  // 8-column vectors per output row
     const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
+    // every lane runs every pass (rows past the tile only skip their
+    // stores) so that the 16 lanes of a row can reduce the FP8 group amax
     for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
       const int r = idx / VPR, cv = idx % VPR;
-      if (r >= rows) continue;
+      const bool valid = r < rows;
       const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
       const uint4 uv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + BN / 2 + cv * 8);
       const int64_t row = row0 + r;
-      const float wr = p.w[row];
       const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-      uint32_t ow[4];
+      if (valid) {
+        const float wr = p.w[row];
+        uint32_t ow[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float a0 = gated_act(p.act_kind, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
-                                   p.beta, p.lbeta, p.clamp) * wr;
-        const float a1 = gated_act(p.act_kind, __uint_as_float(gw[q] & 0xffff0000u),
-                                   __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
-        ow[q] = static_cast<uint32_t>(f32_to_bf16_bits(a0)) | (static_cast<uint32_t>(f32_to_bf16_bits(a1)) << 16);
+        for (int q = 0; q < 4; ++q) {
+          const float a0 = gated_act(p.act_kind, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
+                                     p.beta, p.lbeta, p.clamp) * wr;
+          const float a1 = gated_act(p.act_kind, __uint_as_float(gw[q] & 0xffff0000u),
+                                     __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
+          ow[q] = pack_bf16x2(a0, a1);
+        }
+        *reinterpret_cast<uint4*>(p.c + row * p.ldc + jbase + cv * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
       }
-      *reinterpret_cast<uint4*>(p.c + row * p.ldc + jbase + cv * 8) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
-      if (p.fc1_out) {
-        bf16* fo = p.fc1_out + row * ldf + jbase + cv * 8;
-        *reinterpret_cast<uint4*>(fo) = gv;
-        *reinterpret_cast<uint4*>(fo + p.inter) = uv;
+      if (!p.fc1_out) continue;
+      if (p.fc1_fmt == MM_FC1_BF16) {
+        if (valid) {
+          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          *reinterpret_cast<uint4*>(fo) = gv;
+          *reinterpret_cast<uint4*>(fo + p.inter) = uv;
+        }
+      } else if (p.fc1_fmt == MM_FC1_FP16) {
+        uint32_t gh[4], uh[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          gh[q] = pack_f16x2(__uint_as_float(gw[q] << 16), __uint_as_float(gw[q] & 0xffff0000u));
+          uh[q] = pack_f16x2(__uint_as_float(uw[q] << 16), __uint_as_float(uw[q] & 0xffff0000u));
+        }
+        if (valid) {
+          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          *reinterpret_cast<uint4*>(fo) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
+          *reinterpret_cast<uint4*>(fo + p.inter) = make_uint4(uh[0], uh[1], uh[2], uh[3]);
+        }
+      } else {
+        // FP8: one scale per row per BN/2 = MM_FC1_SCALE_GROUP columns of gate
+        // (and of up), i.e. per row of this tile; the row's 16 lanes reduce
+        // the amax of |bf16 value| with xor shuffles
+        static_assert(BN / 2 == MM_FC1_SCALE_GROUP || EPI != EPI_GATED || BN != 256, "scale group = tile half");
+        float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ga = fmaxf(ga, fmaxf(fabsf(__uint_as_float(gw[q] << 16)), fabsf(__uint_as_float(gw[q] & 0xffff0000u))));
+          ua = fmaxf(ua, fmaxf(fabsf(__uint_as_float(uw[q] << 16)), fabsf(__uint_as_float(uw[q] & 0xffff0000u))));
+        }
+#pragma unroll
+        for (int off = 1; off < VPR; off <<= 1) {
+          ga = fmaxf(ga, __shfl_xor(ga, off));
+          ua = fmaxf(ua, __shfl_xor(ua, off));
+        }
+        const float gs = ga > 0.0f ? ga : 1.0f, us = ua > 0.0f ? ua : 1.0f;
+        const float gm = kFp8Max / gs, um = kFp8Max / us;
+        uint32_t gq[2] = {0, 0}, uq[2] = {0, 0};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t g0 = f32_to_e4m3fn(__uint_as_float(gw[q] << 16) * gm);
+          const uint32_t g1 = f32_to_e4m3fn(__uint_as_float(gw[q] & 0xffff0000u) * gm);
+          const uint32_t u0 = f32_to_e4m3fn(__uint_as_float(uw[q] << 16) * um);
+          const uint32_t u1 = f32_to_e4m3fn(__uint_as_float(uw[q] & 0xffff0000u) * um);
+          gq[q >> 1] |= (g0 | (g1 << 8)) << ((q & 1) * 16);
+          uq[q >> 1] |= (u0 | (u1 << 8)) << ((q & 1) * 16);
+        }
+        if (valid) {
+          uint8_t* fo = static_cast<uint8_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          *reinterpret_cast<uint2*>(fo) = make_uint2(gq[0], gq[1]);
+          *reinterpret_cast<uint2*>(fo + p.inter) = make_uint2(uq[0], uq[1]);
+          if (cv == 0) {
+            const int groups = p.inter / MM_FC1_SCALE_GROUP;
+            float* sc = p.fc1_scale + row * (2 * groups) + nt;
+            sc[0] = gs / kFp8Max;
+            sc[groups] = us / kFp8Max;
+          }
+        }
       }
     }
   }
@@ -934,14 +994,19 @@ extern "C" size_t mm_gemm_workspace_bytes(int64_t max_rows, int32_t num_experts)
 extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send_token, const uint16_t* w1,
                              const int32_t* offsets, const float* weight_perm, int32_t num_experts,
                              int64_t max_rows, int32_t hidden, int32_t inter, int32_t act_kind, float situ_beta,
-                             float situ_linear_beta, float clamp_limit, uint16_t* act, uint16_t* fc1_out,
-                             void* workspace, size_t workspace_bytes, mm_stream_t stream) {
+                             float situ_linear_beta, float clamp_limit, uint16_t* act, void* fc1_out,
+                             int32_t fc1_format, float* fc1_scale, void* workspace, size_t workspace_bytes,
+                             mm_stream_t stream) {
   MM_CHECK_ARG(x && w1 && offsets && weight_perm && act, "mm_fc1_swiglu: null pointer");
   MM_CHECK_ARG(num_experts > 0 && max_rows >= 0 && max_rows < (int64_t(1) << 31), "mm_fc1_swiglu: bad sizes");
   MM_CHECK_ARG(hidden > 0 && hidden % BK == 0, "mm_fc1_swiglu: hidden must be a multiple of %d", BK);
   MM_CHECK_ARG(inter > 0 && inter % 64 == 0, "mm_fc1_swiglu: inter must be a multiple of 64");
   MM_CHECK_ARG(ldx % 8 == 0 && al16(x) && al16(w1), "mm_fc1_swiglu: 16-byte alignment required");
   MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_fc1_swiglu: bad act_kind");
+  MM_CHECK_ARG(fc1_format >= MM_FC1_BF16 && fc1_format <= MM_FC1_FP8, "mm_fc1_swiglu: bad fc1_format");
+  MM_CHECK_ARG(!fc1_out || fc1_format != MM_FC1_FP8 || (fc1_scale && inter % MM_FC1_SCALE_GROUP == 0),
+               "mm_fc1_swiglu: FP8 fc1_out needs fc1_scale and inter %% %d == 0", MM_FC1_SCALE_GROUP);
+  MM_CHECK_ARG(!fc1_out || (reinterpret_cast<uintptr_t>(fc1_out) & 7u) == 0, "mm_fc1_swiglu: fc1_out alignment");
   if (!workspace || workspace_bytes < tile_list_bytes(max_rows, num_experts)) {
     mm_set_error("mm_fc1_swiglu: workspace too small");
     return MM_E_WS;
@@ -960,7 +1025,9 @@ extern "C" int mm_fc1_swiglu(const uint16_t* x, int64_t ldx, const int32_t* send
   p.c = reinterpret_cast<bf16*>(act);
   p.ldc = inter;
   p.w = weight_perm;
-  p.fc1_out = reinterpret_cast<bf16*>(fc1_out);
+  p.fc1_out = fc1_out;
+  p.fc1_fmt = fc1_format;
+  p.fc1_scale = fc1_scale;
   p.inter = inter;
   p.act_kind = act_kind;
   p.beta = situ_beta;

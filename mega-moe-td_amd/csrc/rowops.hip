@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 // ---------------------------------------------------------------- errors
@@ -166,40 +168,82 @@ __device__ __forceinline__ void act_pair(int kind, float a, float b, float beta,
   }
 }
 
-template <int KIND>
+// 8 consecutive saved FC1 values (bf16 / fp16 / fp8 e4m3) of one row -> fp32;
+// v indexes 8-value vectors of the row, fp8 values are scaled by `sc`.
+template <int FMT>
+struct Fc1Row {
+  static constexpr int BYTES = FMT == MM_FC1_FP8 ? 8 : 16;  // bytes per 8 values
+  typedef typename std::conditional<FMT == MM_FC1_FP8, uint2, uint4>::type Vec;
+  __device__ static Vec load(const uint8_t* row, int v) { return reinterpret_cast<const Vec*>(row)[v]; }
+  __device__ static Vec zero() {
+    if constexpr (FMT == MM_FC1_FP8) return make_uint2(0, 0);
+    else return make_uint4(0, 0, 0, 0);
+  }
+  __device__ static void to_f32(const Vec& x, float sc, float* f) {
+    if constexpr (FMT == MM_FC1_BF16) {
+      vec8_to_f32(x, f);
+    } else if constexpr (FMT == MM_FC1_FP16) {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const h2 h = __builtin_bit_cast(h2, w[i]);
+        f[2 * i] = static_cast<float>(h[0]);
+        f[2 * i + 1] = static_cast<float>(h[1]);
+      }
+    } else {
+      const uint32_t w[2] = {x.x, x.y};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = e4m3fn_to_f32((w[i >> 2] >> ((i & 3) * 8)) & 0xffu) * sc;
+    }
+  }
+};
+
+template <int KIND, int FMT>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
-    const uint4* __restrict__ ga, int64_t ld_ga_v, const uint4* __restrict__ fc1, int64_t ld_fc1_v,
-    const float* __restrict__ scale, const int32_t* __restrict__ offsets, int E, int inter_v,
-    float beta, float lbeta, float L, uint4* __restrict__ dab, uint16_t* __restrict__ dscale) {
+    const uint4* __restrict__ ga, int64_t ld_ga_v, const uint8_t* __restrict__ fc1, int64_t ld_fc1,
+    const float* __restrict__ fc1_scale, const float* __restrict__ scale, const int32_t* __restrict__ offsets,
+    int E, int inter_v, float beta, float lbeta, float L, uint4* __restrict__ dab, uint16_t* __restrict__ dscale) {
+  using F = Fc1Row<FMT>;
   constexpr int kind = KIND;
   const int nvalid = offsets[E];
   const int lane = threadIdx.x & 63;
+  const int groups = inter_v * 8 / MM_FC1_SCALE_GROUP;  // FP8 scale groups per half row
   for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
        row += gridDim.x * kRowsPerBlock) {
     const float s = round_bf16(scale[row]);
     const uint4* g_row = ga + static_cast<int64_t>(row) * ld_ga_v;
-    const uint4* a_row = fc1 + static_cast<int64_t>(row) * ld_fc1_v;
-    uint4* d_row = dab + static_cast<int64_t>(row) * ld_fc1_v;
+    const uint8_t* a_row = fc1 + static_cast<int64_t>(row) * ld_fc1 * (FMT == MM_FC1_FP8 ? 1 : 2);
+    const uint8_t* b_row = a_row + static_cast<int64_t>(inter_v) * F::BYTES;
+    const float* sc_row = FMT == MM_FC1_FP8 ? fc1_scale + static_cast<int64_t>(row) * 2 * groups : nullptr;
+    uint4* d_row = dab + static_cast<int64_t>(row) * 2 * inter_v;
     float part = 0.0f;
-    // two 16-byte vectors per lane per pass: all six loads issue before the math
+    // two 8-value vectors per lane per pass: all six loads issue before the math
     for (int v0 = lane; v0 < inter_v; v0 += 128) {
-      uint4 gv[2], av[2], bv[2];
+      uint4 gv[2];
+      typename F::Vec av[2], bv[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int v = v0 + 64 * u;
         const bool in = v < inter_v;
         gv[u] = in ? g_row[v] : make_uint4(0, 0, 0, 0);
-        av[u] = in ? a_row[v] : make_uint4(0, 0, 0, 0);
-        bv[u] = in ? a_row[inter_v + v] : make_uint4(0, 0, 0, 0);
+        av[u] = in ? F::load(a_row, v) : F::zero();
+        bv[u] = in ? F::load(b_row, v) : F::zero();
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int v = v0 + 64 * u;
         if (v >= inter_v) break;
+        float sa = 1.0f, sb = 1.0f;
+        if constexpr (FMT == MM_FC1_FP8) {
+          const int grp = v * 8 / MM_FC1_SCALE_GROUP;
+          sa = sc_row[grp];
+          sb = sc_row[groups + grp];
+        }
         float dc[8], a[8], b[8], da[8], db[8];
         vec8_to_f32(gv[u], dc);
-        vec8_to_f32(av[u], a);
-        vec8_to_f32(bv[u], b);
+        F::to_f32(av[u], sa, a);
+        F::to_f32(bv[u], sb, b);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           float act_a, dact_a, vv, dv;
@@ -269,28 +313,41 @@ extern "C" int mm_gather_route_grad(const uint16_t* dscale, const int32_t* route
   return mm_check_launch("mm_gather_route_grad");
 }
 
-extern "C" int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga, const uint16_t* fc1_out, int64_t ld_fc1,
-                             const float* scale, const int32_t* offsets, int32_t num_experts, int64_t max_rows,
-                             int32_t inter, int32_t act_kind, float situ_beta, float situ_linear_beta,
-                             float clamp_limit, uint16_t* dab, uint16_t* dscale, mm_stream_t stream) {
+extern "C" int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga, const void* fc1_out, int64_t ld_fc1,
+                             int32_t fc1_format, const float* fc1_scale, const float* scale,
+                             const int32_t* offsets, int32_t num_experts, int64_t max_rows, int32_t inter,
+                             int32_t act_kind, float situ_beta, float situ_linear_beta, float clamp_limit,
+                             uint16_t* dab, uint16_t* dscale, mm_stream_t stream) {
   MM_CHECK_ARG(grad_act && fc1_out && scale && offsets && dab && dscale, "mm_swiglu_bwd: null pointer");
   MM_CHECK_ARG(num_experts > 0 && inter > 0 && max_rows >= 0, "mm_swiglu_bwd: bad sizes");
-  MM_CHECK_ARG(inter % 8 == 0 && ld_ga % 8 == 0 && ld_fc1 % 8 == 0 && ld_fc1 >= 2 * inter && ld_ga >= inter,
+  MM_CHECK_ARG(fc1_format >= MM_FC1_BF16 && fc1_format <= MM_FC1_FP8, "mm_swiglu_bwd: bad fc1_format");
+  MM_CHECK_ARG(fc1_format != MM_FC1_FP8 || (fc1_scale && inter % MM_FC1_SCALE_GROUP == 0),
+               "mm_swiglu_bwd: FP8 fc1_out needs fc1_scale and inter %% %d == 0", MM_FC1_SCALE_GROUP);
+  MM_CHECK_ARG(inter % 8 == 0 && ld_ga % 8 == 0 && ld_fc1 % 16 == 0 && ld_fc1 >= 2 * inter && ld_ga >= inter,
                "mm_swiglu_bwd: rows must be 16-byte aligned");
   MM_CHECK_ARG(aligned16(grad_act) && aligned16(fc1_out) && aligned16(dab), "mm_swiglu_bwd: misaligned");
   MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_swiglu_bwd: bad act_kind");
   if (max_rows == 0) return MM_OK;
   auto launch = [&](auto kernel) {
     kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
-        reinterpret_cast<const uint4*>(grad_act), ld_ga / 8, reinterpret_cast<const uint4*>(fc1_out),
-        ld_fc1 / 8, scale, offsets, num_experts, inter / 8, situ_beta, situ_linear_beta, clamp_limit,
+        reinterpret_cast<const uint4*>(grad_act), ld_ga / 8, static_cast<const uint8_t*>(fc1_out), ld_fc1,
+        fc1_scale, scale, offsets, num_experts, inter / 8, situ_beta, situ_linear_beta, clamp_limit,
         reinterpret_cast<uint4*>(dab), dscale);
   };
+  auto by_format = [&](auto kind_tag) {
+    constexpr int K = decltype(kind_tag)::value;
+    if (fc1_format == MM_FC1_BF16)
+      launch(swiglu_bwd_kernel<K, MM_FC1_BF16>);
+    else if (fc1_format == MM_FC1_FP16)
+      launch(swiglu_bwd_kernel<K, MM_FC1_FP16>);
+    else
+      launch(swiglu_bwd_kernel<K, MM_FC1_FP8>);
+  };
   if (act_kind == MM_ACT_SWIGLU)
-    launch(swiglu_bwd_kernel<MM_ACT_SWIGLU>);
+    by_format(std::integral_constant<int, MM_ACT_SWIGLU>());
   else if (act_kind == MM_ACT_CLAMP_SWIGLU)
-    launch(swiglu_bwd_kernel<MM_ACT_CLAMP_SWIGLU>);
+    by_format(std::integral_constant<int, MM_ACT_CLAMP_SWIGLU>());
   else
-    launch(swiglu_bwd_kernel<MM_ACT_SITUGLU>);
+    by_format(std::integral_constant<int, MM_ACT_SITUGLU>());
   return mm_check_launch("mm_swiglu_bwd");
 }

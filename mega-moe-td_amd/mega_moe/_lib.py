@@ -17,6 +17,9 @@ _LIB_PATH = os.environ.get("MEGAMOE_LIB") or os.path.join(os.path.dirname(os.pat
 
 # Activation kinds (include/megamoe.h MM_ACT_*).
 ACT_KINDS = {"swiglu": 0, "situglu": 1, "clamp_swiglu": 2}
+# saved FC1 output formats (MM_FC1_* in include/megamoe.h) and the FP8 scale group
+FC1_FORMATS = {"bf16": 0, "fp16": 1, "fp8": 2}
+FC1_SCALE_GROUP = 128
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -34,15 +37,15 @@ SIGNATURES = {
     "mm_gemm_workspace_bytes": (_SZ, [_I64, _I32]),
     "mm_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "mm_fc1_swiglu": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I32, _I32, _I32,
-                                     _F32, _F32, _F32, _P, _P, _P, _SZ, _P]),
+                                     _F32, _F32, _F32, _P, _P, _I32, _P, _P, _SZ, _P]),
     "mm_grouped_gemm": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _I32,
                                        _I32, _P, _I64, _P, _SZ, _P]),
     "mm_grouped_wgrad": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _P, _P,
                                         _SZ, _P]),
     "mm_combine": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _I32, _P, _I64, _P]),
     "mm_gather_route_grad": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
-    "mm_swiglu_bwd": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _F32, _F32,
-                                     _F32, _P, _P, _P]),
+    "mm_swiglu_bwd": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _P, _P, _P, _I32, _I64, _I32, _I32, _F32,
+                                     _F32, _F32, _P, _P, _P]),
 }
 
 _lib = None

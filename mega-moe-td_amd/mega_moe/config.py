@@ -15,10 +15,13 @@ it unchanged. What the fields mean on MI355X:
   enforced.
 * ``activation`` / ``situ_beta`` / ``situ_linear_beta`` / ``clamp_limit`` select
   the gated activation fused into the FC1 epilogue and its backward.
-* ``save_fc1_dtype`` other than ``"bf16"``, ``enable_moonep`` and the MoonEP
-  knobs are accepted for source compatibility; expert-parallel replica
-  balancing is out of scope on one GPU, so ``enable_moonep=True`` raises
-  ``NotImplementedError`` when the operator is built.
+* ``save_fc1_dtype`` selects the saved raw FC1 output format: ``"bf16"``,
+  ``"fp16"`` (the bf16 values as fp16) or ``"fp8"`` (E4M3 with one fp32 scale
+  per row and per 128-column group; needs ``fc1_gemm_block_size_n=256``).
+* ``enable_moonep`` and the MoonEP knobs are accepted for source
+  compatibility; expert-parallel replica balancing is out of scope on one
+  GPU, so ``enable_moonep=True`` raises ``NotImplementedError`` when the
+  operator is built.
 """
 
 from dataclasses import dataclass, field

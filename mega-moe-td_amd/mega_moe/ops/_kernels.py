@@ -47,25 +47,47 @@ def permute(x: torch.Tensor, send_token: torch.Tensor, offsets: torch.Tensor, ma
     return out
 
 
+_FC1_TORCH_DTYPE = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp8": torch.float8_e4m3fn}
+
+
+def fc1_format_of(t: torch.Tensor) -> str:
+    """Saved-FC1 format name of a tensor's dtype."""
+    for name, dt in _FC1_TORCH_DTYPE.items():
+        if t.dtype == dt:
+            return name
+    raise TypeError(f"fc1_output dtype {t.dtype} is not bf16, fp16 or float8_e4m3fn")
+
+
 def fc1_swiglu(x, send_token, w1, offsets, weight_perm, max_rows: int, activation: str, situ_beta: float,
-               situ_linear_beta, clamp_limit: float, save_fc1: bool):
-    """FC1 grouped GEMM + weighted gated activation -> (act [rows, I], fc1_output [rows, 2I] | None)."""
+               situ_linear_beta, clamp_limit: float, save_fc1: bool, fc1_dtype: str = "bf16"):
+    """FC1 grouped GEMM + weighted gated activation.
+
+    Returns (act [rows, I] bf16, fc1_output [rows, 2I] in ``fc1_dtype`` | None,
+    fc1_scale [rows, 2I / 128] fp32 for fp8 | None).
+    """
     _check_bf16("x", x)
     _check_bf16("w1", w1)
     num_experts, hidden, two_inter = w1.shape
     inter = two_inter // 2
     if x.shape[1] != hidden or not w1.is_contiguous() or x.stride(1) != 1:
         raise ValueError("fc1_swiglu: x [*, H] and contiguous w1 [E, H, 2I] required")
+    if fc1_dtype not in _FC1_TORCH_DTYPE:
+        raise ValueError(f"fc1_dtype must be one of {sorted(_FC1_TORCH_DTYPE)}, got {fc1_dtype!r}")
     dev = x.device
     act = torch.empty(max_rows, inter, dtype=torch.bfloat16, device=dev)
-    fc1_out = torch.empty(max_rows, two_inter, dtype=torch.bfloat16, device=dev) if save_fc1 else None
+    fc1_out = torch.empty(max_rows, two_inter, dtype=_FC1_TORCH_DTYPE[fc1_dtype], device=dev) if save_fc1 else None
+    fc1_scale = None
+    if save_fc1 and fc1_dtype == "fp8":
+        if inter % _lib.FC1_SCALE_GROUP:
+            raise ValueError(f"fp8 fc1 save needs ffn % {_lib.FC1_SCALE_GROUP} == 0, got {inter}")
+        fc1_scale = torch.empty(max_rows, two_inter // _lib.FC1_SCALE_GROUP, dtype=torch.float32, device=dev)
     ws = _gemm_ws(dev, max_rows, num_experts)
     lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
     _lib.call("mm_fc1_swiglu", _lib.ptr(x), x.stride(0), _lib.ptr(send_token), _lib.ptr(w1), _lib.ptr(offsets),
               _lib.ptr(weight_perm), num_experts, max_rows, hidden, inter, _lib.ACT_KINDS[activation],
-              float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(act), _lib.ptr(fc1_out), _lib.ptr(ws),
-              ws.numel(), _lib.stream_of(dev))
-    return act, fc1_out
+              float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(act), _lib.ptr(fc1_out),
+              _lib.FC1_FORMATS[fc1_dtype], _lib.ptr(fc1_scale), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev))
+    return act, fc1_out, fc1_scale
 
 
 def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_rows: int, n: int, k: int):
@@ -112,19 +134,29 @@ def combine(y, route_to_send, num_tokens: int, top_k: int) -> torch.Tensor:
 
 
 def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str, situ_beta: float,
-               situ_linear_beta, clamp_limit: float):
-    """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16)."""
+               situ_linear_beta, clamp_limit: float, fc1_scale=None):
+    """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16).
+
+    ``fc1_out`` is the saved raw FC1 output in bf16, fp16 or float8_e4m3fn
+    (then with its fp32 ``fc1_scale`` [rows, 2I / 128]).
+    """
     _check_bf16("grad_act", grad_act)
-    _check_bf16("fc1_out", fc1_out)
+    fmt = fc1_format_of(fc1_out)
+    if fc1_out.device.type != "cuda" or fc1_out.stride(1) != 1:
+        raise ValueError("fc1_out must be a HIP device tensor with unit column stride")
     inter = fc1_out.shape[1] // 2
+    if fmt == "fp8":
+        if fc1_scale is None or fc1_scale.dtype != torch.float32 or not fc1_scale.is_contiguous() or \
+                tuple(fc1_scale.shape) != (fc1_out.shape[0], 2 * inter // _lib.FC1_SCALE_GROUP):
+            raise ValueError("fp8 fc1_out needs an fp32 contiguous fc1_scale [rows, 2F // 128]")
     dev = fc1_out.device
     dab = torch.empty(max_rows, 2 * inter, dtype=torch.bfloat16, device=dev)
     dscale = torch.empty(max_rows, dtype=torch.bfloat16, device=dev)
     lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
     _lib.call("mm_swiglu_bwd", _lib.ptr(grad_act), grad_act.stride(0), _lib.ptr(fc1_out), fc1_out.stride(0),
-              _lib.ptr(scale), _lib.ptr(offsets), offsets.numel() - 1, max_rows, inter,
-              _lib.ACT_KINDS[activation], float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(dab),
-              _lib.ptr(dscale), _lib.stream_of(dev))
+              _lib.FC1_FORMATS[fmt], _lib.ptr(fc1_scale if fmt == "fp8" else None), _lib.ptr(scale),
+              _lib.ptr(offsets), offsets.numel() - 1, max_rows, inter, _lib.ACT_KINDS[activation],
+              float(situ_beta), lbeta, float(clamp_limit), _lib.ptr(dab), _lib.ptr(dscale), _lib.stream_of(dev))
     return dab, dscale
 
 

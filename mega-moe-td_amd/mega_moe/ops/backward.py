@@ -63,7 +63,14 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     tm.end()
     # step 2: gated-activation backward
     tm.begin("swiglu_bwd")
-    dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R, **act_kw)
+    fc1_scale = None
+    if saved["fc1_output"].dtype == torch.float8_e4m3fn:
+        # FP8 save: dequantize at the load (reference kernels/mega_bwd.py:3185-3206)
+        fc1_scale = saved.get("fc1_output_scale")
+        if fc1_scale is None or int(saved.get("fc1_scale_group_size", 0)) != 128:
+            raise ValueError("an FP8 fc1_output needs fc1_output_scale with fc1_scale_group_size 128")
+    dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
+                               fc1_scale=fc1_scale, **act_kw)
     tm.end()
     # step 3: FC2 wgrad  dW2[e][h, f] = sum_i gco[i, h] act[i, f]
     tm.begin("fc2_wgrad")

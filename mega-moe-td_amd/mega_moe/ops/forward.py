@@ -96,8 +96,11 @@ class FusedMoEForward(torch.nn.Module):
         self.config = config if config is not None else MoEForwardConfig()
         if self.config.enable_moonep:
             raise NotImplementedError("MoonEP replica balancing is multi-GPU and not built")
-        if self.config.save_fc1_dtype != "bf16":
-            raise NotImplementedError("only save_fc1_dtype='bf16' is built")
+        if self.config.save_fc1_dtype == "fp8" and self.config.fc1_gemm_block_size_n != 256:
+            # the FP8 save carries one scale per fc1_gemm_block_size_n // 2 columns; the
+            # device kernels fix that group at 128 (the reference default block of 256)
+            raise NotImplementedError("save_fc1_dtype='fp8' is built for fc1_gemm_block_size_n=256 "
+                                      "(128-column scale groups)")
         self.enable_moonep = False
         self.enable_single_kernel_forward = self.config.enable_single_kernel_forward
         self.physical_experts_per_rank = self.experts_per_rank
@@ -334,9 +337,10 @@ class FusedMoEForward(torch.nn.Module):
             tables = self._route(selected_experts, routing_weights)
             tm.end()
             tm.begin("fc1_swiglu")
-            act, fc1_out = K.fc1_swiglu(hidden_states, tables.send_token, gate_up_weight, tables.offsets,
-                                        tables.weight_perm, num_routes, self.activation, self.situ_beta,
-                                        self.situ_linear_beta, self.clamp_limit, save_fc1=return_saved)
+            act, fc1_out, fc1_scale = K.fc1_swiglu(
+                hidden_states, tables.send_token, gate_up_weight, tables.offsets, tables.weight_perm, num_routes,
+                self.activation, self.situ_beta, self.situ_linear_beta, self.clamp_limit, save_fc1=return_saved,
+                fc1_dtype=self.config.save_fc1_dtype)
             tm.end()
             tm.begin("fc2")
             se, sh, sf = down_weight.stride()
@@ -366,6 +370,10 @@ class FusedMoEForward(torch.nn.Module):
                 route_to_send=tables.route_to_send, recv_weights_sorted=tables.weight_perm,
                 fc1_output=fc1_out, swiglu_out_weighted=act,
             )
+            if fc1_scale is not None:
+                # FP8 save (reference ops/forward.py:1874-1880): one fp32 scale per row and
+                # per 128-column group, gate groups then up groups
+                saved.update(fc1_output_scale=fc1_scale, fc1_scale_group_size=128)
         return out, saved
 
 

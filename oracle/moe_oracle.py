@@ -16,6 +16,9 @@ A restatement, written for this repository, of the reference's algorithm:
               fp32, FC2 rounded to bf16, combine = fp32 sum over the k slots in
               slot order, rounded to bf16. The gated activation variants follow
               ops/_torch_forward.py:177-205.
+* saved FC1   save_fc1_dtype bf16 / fp16 / fp8 (E4M3 + per-row, per-128-
+              column fp32 scales) per kernels/fused_forward.py:888-937, read
+              back per kernels/mega_bwd.py:264-270.
 * backward    tests/_moe_baselines.py:96-226 (moe_backward_torch) at one
               rank, swiglu_bwd per tests/_moe_baselines.py:122-160 and
               kernels/swiglu_bwd.py:52-83 (scale = the bf16-cast routing
@@ -27,7 +30,10 @@ pure-Python brute-force stable sort plus the reference's invariants
 (tests/function/test_single_kernel_stable_scatter.py); the forward against a
 per-token fp64 dense evaluation; combine with integer-valued rows (exact);
 the backward against torch.autograd of an fp64 restatement of the forward
-(as src/mega_moe/_goldens/backward.py:200-283 cross-checks it).
+(as src/mega_moe/_goldens/backward.py:200-283 cross-checks it); the FP8
+quantizer against the closed-form E4M3 value of every code (round trip,
+ties-to-even at every midpoint, saturation) and its per-group invariants
+(max |q| = 448, error <= half an E4M3 step).
 """
 
 from __future__ import annotations
@@ -105,9 +111,61 @@ def gated_act_grad(g, u, activation="swiglu", situ_beta=1.0, situ_linear_beta=No
     return act_a, dact, u, torch.ones_like(u)
 
 
+# --------------------------------------------------------------------- saved FC1 formats
+FP8_MAX = 448.0          # largest finite E4M3 ("fn") value
+FC1_SCALE_GROUP = 128    # columns per FP8 scale (fc1_gemm_block_size_n // 2 at its default 256)
+
+
+def e4m3fn_value(code: int) -> float:
+    """Closed-form value of an 8-bit E4M3 "fn" code (bias 7, no infinities,
+    0x7F / 0xFF = NaN): the definition the quantizer below is pinned to."""
+    sign = -1.0 if code & 0x80 else 1.0
+    e, m = (code >> 3) & 0xF, code & 7
+    if e == 15 and m == 7:
+        return float("nan")
+    if e == 0:
+        return sign * m * 2.0 ** -9
+    return sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def quantize_fc1(gu: torch.Tensor, fmt: str):
+    """Saved form of the raw FC1 output gu [M, 2I] (bf16 values held in fp32).
+
+    bf16 / fp16: the values cast (kernels/fused_forward.py:888-901).
+    fp8: per row and per 128-column group (gate groups, then up groups),
+    amax = max |value| (1 for an all-zero group), q = E4M3(value * (448 /
+    amax)) rounded to nearest even and saturated at 448, scale = amax / 448
+    (kernels/fused_forward.py:902-937). Returns (stored, scale | None).
+    """
+    if fmt == "bf16":
+        return gu.to(torch.bfloat16), None
+    if fmt == "fp16":
+        return gu.to(torch.float16), None
+    if fmt != "fp8":
+        raise ValueError(fmt)
+    M, two_i = gu.shape
+    g = gu.float().reshape(M, two_i // FC1_SCALE_GROUP, FC1_SCALE_GROUP)
+    amax = g.abs().amax(dim=2)
+    safe = torch.where(amax > 0, amax, torch.ones_like(amax))
+    # correctly rounded fp32 division (a python-scalar / tensor expression
+    # would be evaluated as scalar * reciprocal(tensor), one more rounding)
+    mult = torch.full_like(safe, FP8_MAX) / safe
+    q = (g * mult[..., None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.reshape(M, two_i), safe / FP8_MAX
+
+
+def dequantize_fc1(stored: torch.Tensor, scale=None) -> torch.Tensor:
+    """fp32 values of a saved FC1 output (value = e4m3 * scale for fp8;
+    kernels/mega_bwd.py:264-270)."""
+    if stored.dtype == torch.float8_e4m3fn:
+        M, two_i = stored.shape
+        return (stored.float().reshape(M, -1, FC1_SCALE_GROUP) * scale[..., None]).reshape(M, two_i)
+    return stored.float()
+
+
 # --------------------------------------------------------------------- forward
 def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, situ_linear_beta=None,
-            clamp_limit=7.0):
+            clamp_limit=7.0, save_fc1_dtype="bf16"):
     """Layer forward on CPU.
 
     x [T, H] bf16; selected [T, k] int32; gate_up [E, H, 2I] bf16;
@@ -150,9 +208,10 @@ def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, 
         rows = r2s[:, j]
         m = rows >= 0
         out[m] += y[rows[m]]
+    fc1_saved, fc1_scale = quantize_fc1(torch.cat([gate, up], dim=1), save_fc1_dtype)
     state = dict(tables=tb, x=xf, w1=w1, w2=w2, wp=wp, gate=gate, up=up, act=act, y=y, T=T, k=k, E=E,
                  inter=inter, activation=activation, situ_beta=situ_beta, situ_linear_beta=situ_linear_beta,
-                 clamp_limit=clamp_limit)
+                 clamp_limit=clamp_limit, fc1_output=fc1_saved, fc1_output_scale=fc1_scale)
     return out.to(torch.bfloat16), state
 
 
@@ -199,7 +258,8 @@ def backward(state, dy):
         if a < b:
             grad_act[a:b] = bf16(gco[a:b] @ w2[e])
     scale = bf16(state["wp"])[:, None]                            # step 2
-    act_a, dact, v, dv = gated_act_grad(state["gate"], state["up"], state["activation"], state["situ_beta"],
+    gu = dequantize_fc1(state["fc1_output"], state.get("fc1_output_scale"))  # the saved (maybe narrowed) FC1
+    act_a, dact, v, dv = gated_act_grad(gu[:, :inter], gu[:, inter:], state["activation"], state["situ_beta"],
                                         state["situ_linear_beta"], state["clamp_limit"])
     dgate = grad_act * dact * v * scale
     dup = grad_act * act_a * dv * scale

@@ -216,7 +216,8 @@ def test_permute_exact():
 
 
 @pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu", "situglu"])
-def test_swiglu_bwd(activation):
+@pytest.mark.parametrize("fmt", ["bf16", "fp16", "fp8"])
+def test_swiglu_bwd(activation, fmt):
     from mega_moe.ops import _kernels as K
     M, inter = 300, 256
     g = torch.Generator(device=DEV).manual_seed(5)
@@ -226,9 +227,11 @@ def test_swiglu_bwd(activation):
     offs = torch.tensor([0, 100, 290], dtype=torch.int32, device=DEV)
     kw = dict(activation=activation, situ_beta=1.5, situ_linear_beta=2.0 if activation == "situglu" else None,
               clamp_limit=0.5)
-    dab, ds = K.swiglu_bwd(ga, fc1, sc, offs, M, **kw)
+    q, qs = O.quantize_fc1(fc1.float().cpu(), fmt)   # saved form of the FC1 values in this format
+    dab, ds = K.swiglu_bwd(ga, q.to(DEV), sc, offs, M, fc1_scale=None if qs is None else qs.to(DEV), **kw)
     torch.cuda.synchronize()
-    gate, up = fc1[:290, :inter].float().cpu(), fc1[:290, inter:].float().cpu()
+    fcd = O.dequantize_fc1(q, qs)
+    gate, up = fcd[:290, :inter], fcd[:290, inter:]
     act_a, dact, v, dv = O.gated_act_grad(gate, up, **kw)
     s = O.bf16(sc[:290].cpu())[:, None]
     gaf = ga[:290].float().cpu()

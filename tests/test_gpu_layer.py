@@ -180,3 +180,41 @@ def test_all_routes_dropped_and_one_hot_expert():
     assert_rel(out, ref_out, 2e-2, "out")
     for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
         assert_rel(g[name], ref[name], 2e-2, name)
+
+
+@pytest.mark.parametrize("spec", SMALL, ids=lambda s: s.name)
+@pytest.mark.parametrize("fmt", ["fp16", "fp8"])
+def test_saved_fc1_formats(spec, fmt):
+    """save_fc1_dtype fp16 / fp8 (reference config.py:178-186): the saved bytes
+    equal the oracle's narrowing of this build's own bf16 save (bit exact,
+    FP8 scales included), and the backward through the narrow save matches
+    the oracle backward that reads the same format."""
+    inp = make_inputs(spec, device="cuda", seed=21, weight_scale=0.1)
+    sel = inp["selected"].clone()
+    sel[3, 0] = -1
+    args = (inp["x"], sel, inp["gate_up"], inp["down"], inp["rw"])
+    _, sb = _op(spec).forward(*args, return_saved=True)
+    out, sn = _op(spec, save_fc1_dtype=fmt).forward(*args, return_saved=True)
+    g = mega_moe.moe_backward_triton(sn, inp["dy"])
+    torch.cuda.synchronize()
+    n = int(sb["split_size_cum_per_expert"][-1])
+    ref_q, ref_s = O.quantize_fc1(sb["fc1_output"][:n].float().cpu(), fmt)
+    got = sn["fc1_output"][:n].cpu()
+    assert got.dtype == ref_q.dtype
+    assert torch.equal(got.view(torch.uint8) if fmt == "fp8" else got, ref_q.view(torch.uint8) if fmt == "fp8" else ref_q)
+    if fmt == "fp8":
+        assert sn["fc1_scale_group_size"] == 128
+        assert torch.equal(sn["fc1_output_scale"][:n].cpu(), ref_s)
+    else:
+        assert "fc1_output_scale" not in sn
+    ref_out, st = O.forward(inp["x"].cpu(), sel.cpu(), inp["gate_up"].cpu(), inp["down"].cpu(), inp["rw"].cpu(),
+                            save_fc1_dtype=fmt)
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out, ref_out, 2e-2, "output")
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
+        assert_rel(g[name], ref[name], 2e-2, name)
+
+
+def test_fp8_save_needs_default_block():
+    with pytest.raises(NotImplementedError):
+        _op(SMALL[0], save_fc1_dtype="fp8", fc1_gemm_block_size_n=128)

@@ -137,3 +137,100 @@ def test_backward_matches_autograd(activation):
     assert_rel(g["grad_fc2"], ref["grad_fc2"], 2e-2, "grad_fc2")
     # dropped routes get zero routing-weight gradient
     assert g["grad_routing_weights"][0, 0] == 0 and g["grad_routing_weights"][3, 1] == 0
+
+
+# --------------------------------------------------------------------- saved FC1 formats
+def test_e4m3fn_codes_round_trip_through_the_quantizer_cast():
+    """Every finite E4M3 code: its closed-form value converts back to the same
+    code, and the cast's decode equals the closed form."""
+    for code in range(256):
+        v = O.e4m3fn_value(code)
+        if v != v:  # NaN codes 0x7F / 0xFF
+            assert code & 0x7F == 0x7F
+            continue
+        t = torch.tensor([v], dtype=torch.float32).to(torch.float8_e4m3fn)
+        if v == 0.0:
+            assert t.view(torch.uint8).item() in (0x00, 0x80)
+        else:
+            assert t.view(torch.uint8).item() == code, hex(code)
+        assert torch.tensor([code], dtype=torch.uint8).view(torch.float8_e4m3fn).float().item() == v
+
+
+def test_e4m3fn_ties_to_even_and_saturation():
+    pos = [O.e4m3fn_value(c) for c in range(0x7F)]  # 0 .. 448, increasing
+    assert pos == sorted(pos) and pos[-1] == 448.0
+    for c in range(0x7E):
+        lo, hi = pos[c], pos[c + 1]
+        mid = (lo + hi) / 2
+        even = c if c % 2 == 0 else c + 1
+        got = torch.tensor([mid, mid - (hi - lo) / 8, mid + (hi - lo) / 8]).to(torch.float8_e4m3fn).view(torch.uint8)
+        assert got.tolist() == [even, c, c + 1], (c, lo, hi)
+    # the quantizer saturates: clamp then cast
+    q, s = O.quantize_fc1(torch.full((1, 256), 3.0), "fp8")
+    assert torch.all(q.float() == 448.0) and torch.allclose(s, torch.full((1, 2), 3.0 / 448.0))
+
+
+def test_quantize_fc1_fp8_group_invariants():
+    g = torch.Generator().manual_seed(3)
+    I = 256
+    gu = O.bf16(torch.randn(40, 2 * I, generator=g) * torch.logspace(-3, 2, 40)[:, None])
+    gu[7] = 0.0                       # an all-zero row: q = 0, scale = 1/448
+    gu[9, :128] = 0.0                 # one zero group
+    q, s = O.quantize_fc1(gu, "fp8")
+    assert q.dtype == torch.float8_e4m3fn and q.shape == gu.shape and s.shape == (40, 2 * I // 128)
+    qg = q.float().view(40, -1, 128)
+    amax = gu.view(40, -1, 128).abs().amax(2)
+    nz = amax > 0
+    assert torch.all(qg.abs().amax(2)[nz] == 448.0)
+    assert torch.all(qg[~nz] == 0) and torch.all(s[~nz] == 1.0 / 448.0)
+    assert torch.allclose(s[nz], amax[nz] / 448.0, rtol=1e-7, atol=0)
+    # gate groups first, then up groups
+    assert torch.equal(s[:, 0], torch.where(gu[:, :128].abs().amax(1) > 0, gu[:, :128].abs().amax(1), torch.ones(40)) / 448.0)
+    d = O.dequantize_fc1(q, s)
+    err = (d - gu).abs().view(40, -1, 128)
+    bound = gu.view(40, -1, 128).abs() * 2.0 ** -4 + (amax / 448.0 * 2.0 ** -10)[..., None] * 1.001
+    assert torch.all(err <= bound)
+
+
+def test_quantize_fc1_fp16_is_exact_for_bf16_values():
+    g = torch.Generator().manual_seed(4)
+    gu = O.bf16(torch.randn(16, 256, generator=g) * 50)
+    q, s = O.quantize_fc1(gu, "fp16")
+    assert s is None and q.dtype == torch.float16 and torch.equal(q.float(), gu)
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "fp8"])
+def test_backward_with_narrow_fc1_save_stays_close(fmt):
+    """The backward reads the saved FC1 through the narrow format only: fp16
+    keeps the bf16 values exactly, fp8 moves the gradients by at most a few
+    percent of their scale."""
+    T, H, I, E, k = 48, 64, 128, 4, 2
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.1).to(torch.bfloat16)
+    rw = torch.softmax(torch.randn(T, k, generator=g), 1)
+    dy = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    _, st_b = O.forward(x, sel, w1, w2, rw)
+    _, st_n = O.forward(x, sel, w1, w2, rw, save_fc1_dtype=fmt)
+    rb, rn = O.backward(st_b, dy), O.backward(st_n, dy)
+    for key in ("grad_hidden", "grad_gate_up", "grad_routing_weights"):
+        a, b = rn[key].float(), rb[key].float()
+        rel = float((a - b).abs().max() / b.abs().max())
+        if fmt == "fp16":
+            assert rel == 0.0, key
+        else:
+            assert rel < 0.1, (key, rel)
+    assert torch.equal(rn["grad_fc2"], rb["grad_fc2"])  # dW2 does not read the FC1 save
+
+
+def test_quantize_fc1_multiplier_is_correctly_rounded():
+    """448 / amax is one correctly rounded fp32 division (as the device epilogue
+    computes it): for amax = 6, 0.28125 * fp32(448 / 6) is exactly 21, a tie
+    between the E4M3 codes for 20 and 22 that rounds to the even one (20)."""
+    gu = torch.zeros(1, 256)
+    gu[0, 0], gu[0, 1] = 6.0, 0.28125
+    q, s = O.quantize_fc1(gu, "fp8")
+    assert q.view(torch.uint8)[0, 1].item() == 0x5A and q.float()[0, 1].item() == 20.0
+    assert q.float()[0, 0].item() == 448.0 and s[0, 0].item() == torch.tensor(6.0 / 448.0).item()
