@@ -210,6 +210,21 @@ int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga,
                   float situ_beta, float situ_linear_beta, float clamp_limit,
                   uint16_t* dab, uint16_t* dscale, mm_stream_t stream);
 
+/*
+ * Activation recompute from the saved FC1 output (any fc1_format), per
+ * expert-major row i < offsets[E]:
+ *   act[i, j] = bf16(act_fn(gate, up) * weight_perm[i])
+ * — the FC1 epilogue's formula, so for a bf16 save it reproduces the
+ * forward's act bit for bit. Replaces the MOE_SAVED_RECOMPUTE act recompute
+ * of kernels/mega_bwd.py:1414-1468 (_recompute_act_rows).
+ */
+int mm_gated_act(const void* fc1_out, int64_t ld_fc1, int32_t fc1_format,
+                 const float* fc1_scale, const float* weight_perm,
+                 const int32_t* offsets, int32_t num_experts, int64_t max_rows,
+                 int32_t inter, int32_t act_kind, float situ_beta,
+                 float situ_linear_beta, float clamp_limit, uint16_t* act,
+                 int64_t ld_act, mm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

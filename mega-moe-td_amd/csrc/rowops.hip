@@ -262,6 +262,42 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
   }
 }
 
+// act[i] = bf16(act_fn(gate, up) * w[i]) from a saved FC1 row (any format):
+// the FC1 epilogue's formula, bit-identical to the forward's act for a bf16
+// save with the same fp32 weight.
+template <int KIND, int FMT>
+__global__ __launch_bounds__(kThreads) void gated_act_kernel(
+    const uint8_t* __restrict__ fc1, int64_t ld_fc1, const float* __restrict__ fc1_scale,
+    const float* __restrict__ w, const int32_t* __restrict__ offsets, int E, int inter_v, float beta, float lbeta,
+    float L, uint4* __restrict__ act, int64_t ld_act_v) {
+  using F = Fc1Row<FMT>;
+  const int nvalid = offsets[E];
+  const int lane = threadIdx.x & 63;
+  const int groups = inter_v * 8 / MM_FC1_SCALE_GROUP;
+  for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < nvalid;
+       row += gridDim.x * kRowsPerBlock) {
+    const float wr = w[row];
+    const uint8_t* a_row = fc1 + static_cast<int64_t>(row) * ld_fc1 * (FMT == MM_FC1_FP8 ? 1 : 2);
+    const uint8_t* b_row = a_row + static_cast<int64_t>(inter_v) * F::BYTES;
+    const float* sc_row = FMT == MM_FC1_FP8 ? fc1_scale + static_cast<int64_t>(row) * 2 * groups : nullptr;
+    uint4* o_row = act + static_cast<int64_t>(row) * ld_act_v;
+    for (int v = lane; v < inter_v; v += 64) {
+      float sa = 1.0f, sb = 1.0f;
+      if constexpr (FMT == MM_FC1_FP8) {
+        const int grp = v * 8 / MM_FC1_SCALE_GROUP;
+        sa = sc_row[grp];
+        sb = sc_row[groups + grp];
+      }
+      float a[8], b[8], o[8];
+      F::to_f32(F::load(a_row, v), sa, a);
+      F::to_f32(F::load(b_row, v), sb, b);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = gated_act(KIND, a[q], b[q], beta, lbeta, L) * wr;
+      o_row[v] = f32_to_vec8(o);
+    }
+  }
+}
+
 int grid_for_rows(int64_t rows) {
   int64_t g = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
   if (g < 1) g = 1;
@@ -350,4 +386,41 @@ extern "C" int mm_swiglu_bwd(const uint16_t* grad_act, int64_t ld_ga, const void
   else
     by_format(std::integral_constant<int, MM_ACT_SITUGLU>());
   return mm_check_launch("mm_swiglu_bwd");
+}
+
+extern "C" int mm_gated_act(const void* fc1_out, int64_t ld_fc1, int32_t fc1_format, const float* fc1_scale,
+                            const float* weight_perm, const int32_t* offsets, int32_t num_experts, int64_t max_rows,
+                            int32_t inter, int32_t act_kind, float situ_beta, float situ_linear_beta,
+                            float clamp_limit, uint16_t* act, int64_t ld_act, mm_stream_t stream) {
+  MM_CHECK_ARG(fc1_out && weight_perm && offsets && act, "mm_gated_act: null pointer");
+  MM_CHECK_ARG(num_experts > 0 && inter > 0 && max_rows >= 0, "mm_gated_act: bad sizes");
+  MM_CHECK_ARG(fc1_format >= MM_FC1_BF16 && fc1_format <= MM_FC1_FP8, "mm_gated_act: bad fc1_format");
+  MM_CHECK_ARG(fc1_format != MM_FC1_FP8 || (fc1_scale && inter % MM_FC1_SCALE_GROUP == 0),
+               "mm_gated_act: FP8 fc1_out needs fc1_scale and inter %% %d == 0", MM_FC1_SCALE_GROUP);
+  MM_CHECK_ARG(inter % 8 == 0 && ld_fc1 % 16 == 0 && ld_fc1 >= 2 * inter && ld_act % 8 == 0 && ld_act >= inter,
+               "mm_gated_act: rows must be 16-byte aligned");
+  MM_CHECK_ARG(aligned16(fc1_out) && aligned16(act), "mm_gated_act: misaligned");
+  MM_CHECK_ARG(act_kind >= 0 && act_kind <= 2, "mm_gated_act: bad act_kind");
+  if (max_rows == 0) return MM_OK;
+  auto launch = [&](auto kernel) {
+    kernel<<<grid_for_rows(max_rows), kThreads, 0, mm_hip_stream(stream)>>>(
+        static_cast<const uint8_t*>(fc1_out), ld_fc1, fc1_scale, weight_perm, offsets, num_experts, inter / 8,
+        situ_beta, situ_linear_beta, clamp_limit, reinterpret_cast<uint4*>(act), ld_act / 8);
+  };
+  auto by_format = [&](auto kind_tag) {
+    constexpr int K = decltype(kind_tag)::value;
+    if (fc1_format == MM_FC1_BF16)
+      launch(gated_act_kernel<K, MM_FC1_BF16>);
+    else if (fc1_format == MM_FC1_FP16)
+      launch(gated_act_kernel<K, MM_FC1_FP16>);
+    else
+      launch(gated_act_kernel<K, MM_FC1_FP8>);
+  };
+  if (act_kind == MM_ACT_SWIGLU)
+    by_format(std::integral_constant<int, MM_ACT_SWIGLU>());
+  else if (act_kind == MM_ACT_CLAMP_SWIGLU)
+    by_format(std::integral_constant<int, MM_ACT_CLAMP_SWIGLU>());
+  else
+    by_format(std::integral_constant<int, MM_ACT_SITUGLU>());
+  return mm_check_launch("mm_gated_act");
 }

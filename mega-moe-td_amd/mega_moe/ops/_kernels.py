@@ -166,3 +166,21 @@ def gather_route_grad(dscale, route_to_send, shape) -> torch.Tensor:
     _lib.call("mm_gather_route_grad", _lib.ptr(dscale), _lib.ptr(route_to_send), out.numel(), _lib.ptr(out),
               _lib.stream_of(dscale.device))
     return out
+
+
+def gated_act(fc1_out, weight_perm, offsets, max_rows: int, activation: str, situ_beta: float, situ_linear_beta,
+              clamp_limit: float, fc1_scale=None) -> torch.Tensor:
+    """act [rows, I] bf16 recomputed from a saved FC1 output (bf16 / fp16 / fp8 + scale)."""
+    fmt = fc1_format_of(fc1_out)
+    if fc1_out.device.type != "cuda" or fc1_out.stride(1) != 1:
+        raise ValueError("fc1_out must be a HIP device tensor with unit column stride")
+    inter = fc1_out.shape[1] // 2
+    if fmt == "fp8" and (fc1_scale is None or fc1_scale.dtype != torch.float32 or not fc1_scale.is_contiguous()):
+        raise ValueError("fp8 fc1_out needs an fp32 contiguous fc1_scale")
+    act = torch.empty(max_rows, inter, dtype=torch.bfloat16, device=fc1_out.device)
+    lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
+    _lib.call("mm_gated_act", _lib.ptr(fc1_out), fc1_out.stride(0), _lib.FC1_FORMATS[fmt],
+              _lib.ptr(fc1_scale if fmt == "fp8" else None), _lib.ptr(weight_perm), _lib.ptr(offsets),
+              offsets.numel() - 1, max_rows, inter, _lib.ACT_KINDS[activation], float(situ_beta), lbeta,
+              float(clamp_limit), _lib.ptr(act), act.stride(0), _lib.stream_of(fc1_out.device))
+    return act

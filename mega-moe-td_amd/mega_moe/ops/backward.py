@@ -26,6 +26,7 @@ import torch
 
 from ..runtime.timing import NULL_TIMER
 from . import _kernels as K
+from .forward import saved_recompute
 
 
 def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_states=None):
@@ -73,8 +74,15 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
                                fc1_scale=fc1_scale, **act_kw)
     tm.end()
     # step 3: FC2 wgrad  dW2[e][h, f] = sum_i gco[i, h] act[i, f]
+    act = saved.get("swiglu_out_weighted")
+    if act is None or saved_recompute():
+        # MOE_SAVED_RECOMPUTE: act from the saved FC1 output (reference kernels/mega_bwd.py:1414-1468)
+        tm.begin("act_recompute")
+        act = K.gated_act(saved["fc1_output"], saved["recv_weights_sorted"], offsets, R, fc1_scale=fc1_scale,
+                          **act_kw)
+        tm.end()
     tm.begin("fc2_wgrad")
-    grad_fc2 = K.grouped_wgrad(dy, send_token, saved["swiglu_out_weighted"], None, offsets, H, inter)
+    grad_fc2 = K.grouped_wgrad(dy, send_token, act, None, offsets, H, inter)
     tm.end()
     # step 4: FC1 dgrad, B_e(k=j, n=h) = W1[e, h, j]; top-k reduce; gate gather
     tm.begin("fc1_dgrad")

@@ -20,6 +20,8 @@ valid count are never read.
 
 from __future__ import annotations
 
+import os
+
 from dataclasses import dataclass
 from typing import Optional
 
@@ -370,11 +372,21 @@ class FusedMoEForward(torch.nn.Module):
                 route_to_send=tables.route_to_send, recv_weights_sorted=tables.weight_perm,
                 fc1_output=fc1_out, swiglu_out_weighted=act,
             )
+            if saved_recompute():
+                # MOE_SAVED_RECOMPUTE=1 (reference kernels/mega_bwd.py:3208-3226): the backward
+                # recomputes act from fc1_output, so the saved dict does not pin it
+                del saved["swiglu_out_weighted"]
             if fc1_scale is not None:
                 # FP8 save (reference ops/forward.py:1874-1880): one fp32 scale per row and
                 # per 128-column group, gate groups then up groups
                 saved.update(fc1_output_scale=fc1_scale, fc1_scale_group_size=128)
         return out, saved
+
+
+def saved_recompute() -> bool:
+    """``MOE_SAVED_RECOMPUTE=1``: the backward recomputes the weighted
+    activation from ``fc1_output`` instead of reading a saved copy."""
+    return os.environ.get("MOE_SAVED_RECOMPUTE", "0") == "1"
 
 
 def pack_gate_up_weights(gate_weight_local: torch.Tensor, up_weight_local: torch.Tensor) -> torch.Tensor:

@@ -241,8 +241,13 @@ def forward_tokens(x, selected, gate_up, down, rw, tokens, activation="swiglu", 
 
 
 # --------------------------------------------------------------------- backward
-def backward(state, dy):
-    """Five-stage backward on CPU (tests/_moe_baselines.py:96-226)."""
+def backward(state, dy, recompute_act=False):
+    """Five-stage backward on CPU (tests/_moe_baselines.py:96-226).
+
+    ``recompute_act``: the FC2 weight gradient reads the weighted activation
+    recomputed from the saved (maybe narrowed) FC1 output, as the reference's
+    MOE_SAVED_RECOMPUTE mode does (kernels/mega_bwd.py:1414-1468).
+    """
     tb = state["tables"]
     T, k, E, inter = state["T"], state["k"], state["E"], state["inter"]
     offsets = tb["offsets"]
@@ -265,6 +270,10 @@ def backward(state, dy):
     dup = grad_act * act_a * dv * scale
     dab = bf16(torch.cat([dgate, dup], dim=1))
     dscale = bf16((act_a * v * grad_act).sum(dim=1))
+    act_saved = state["act"]
+    if recompute_act:
+        act_saved = bf16(gated_act(gu[:, :inter], gu[:, inter:], state["activation"], state["situ_beta"],
+                                   state["situ_linear_beta"], state["clamp_limit"]) * state["wp"][:, None])
     grad_fc2 = torch.zeros(E, H, inter)                           # step 3
     dx = torch.empty(M, H)
     grad_gate_up = torch.zeros(E, H, 2 * inter)
@@ -273,7 +282,7 @@ def backward(state, dy):
         a, b = int(offsets[e]), int(offsets[e + 1])
         if a == b:
             continue
-        grad_fc2[e] = bf16(gco[a:b].T @ state["act"][a:b])
+        grad_fc2[e] = bf16(gco[a:b].T @ act_saved[a:b])
         dx[a:b] = bf16(dab[a:b] @ w1[e].T)                        # step 4a
         grad_gate_up[e] = bf16(xp[a:b].T @ dab[a:b])              # step 5
     r2s = torch.from_numpy(tb["route_to_send"]).long().view(T, k)

@@ -218,3 +218,47 @@ def test_saved_fc1_formats(spec, fmt):
 def test_fp8_save_needs_default_block():
     with pytest.raises(NotImplementedError):
         _op(SMALL[0], save_fc1_dtype="fp8", fc1_gemm_block_size_n=128)
+
+
+@pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu", "situglu"])
+def test_act_recompute_is_bit_exact_for_bf16_save(activation):
+    """mm_gated_act over the saved bf16 FC1 output reproduces the forward's
+    weighted activation bit for bit."""
+    from mega_moe.ops import _kernels as K
+    spec = SMALL[1]
+    kw = _act_kw(activation)
+    cfg = {k: v for k, v in kw.items() if k != "activation"}
+    inp = make_inputs(spec, device="cuda", seed=31, weight_scale=0.1)
+    _, sv = _op(spec, activation, **cfg).forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"],
+                                                 return_saved=True)
+    act = K.gated_act(sv["fc1_output"], sv["recv_weights_sorted"], sv["split_size_cum_per_expert"],
+                      sv["total_routes"], **kw)
+    torch.cuda.synchronize()
+    n = int(sv["split_size_cum_per_expert"][-1])
+    assert torch.equal(act[:n], sv["swiglu_out_weighted"][:n])
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8"])
+def test_saved_recompute_mode(fmt, monkeypatch):
+    """MOE_SAVED_RECOMPUTE=1: the saved dict drops the weighted activation and
+    the backward recomputes it from fc1_output (bf16: identical gradients;
+    fp8: within tolerance of the oracle reading the same save)."""
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=33, weight_scale=0.1)
+    args = (inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
+    _, s0 = _op(spec, save_fc1_dtype=fmt).forward(*args, return_saved=True)
+    g0 = mega_moe.moe_backward_triton(s0, inp["dy"])
+    monkeypatch.setenv("MOE_SAVED_RECOMPUTE", "1")
+    _, s1 = _op(spec, save_fc1_dtype=fmt).forward(*args, return_saved=True)
+    assert "swiglu_out_weighted" not in s1
+    g1 = mega_moe.moe_backward_triton(s1, inp["dy"])
+    torch.cuda.synchronize()
+    names = ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up")
+    if fmt == "bf16":
+        for name in names:
+            assert torch.equal(g1[name], g0[name]), name
+    else:
+        _, st = O.forward(*(t.cpu() for t in args), save_fc1_dtype=fmt)
+        ref = O.backward(st, inp["dy"].cpu(), recompute_act=True)
+        for name in names:
+            assert_rel(g1[name], ref[name], 2e-2, name)

@@ -234,3 +234,20 @@ def test_quantize_fc1_multiplier_is_correctly_rounded():
     q, s = O.quantize_fc1(gu, "fp8")
     assert q.view(torch.uint8)[0, 1].item() == 0x5A and q.float()[0, 1].item() == 20.0
     assert q.float()[0, 0].item() == 448.0 and s[0, 0].item() == torch.tensor(6.0 / 448.0).item()
+
+
+def test_backward_recompute_act_matches_saved_for_bf16():
+    """With the bf16 save, the recomputed activation equals the saved one, so
+    recompute mode leaves every gradient unchanged."""
+    T, H, I, E, k = 40, 64, 128, 4, 2
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    w1 = (torch.randn(E, H, 2 * I, generator=g) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.1).to(torch.bfloat16)
+    rw = torch.softmax(torch.randn(T, k, generator=g), 1)
+    dy = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    _, st = O.forward(x, sel, w1, w2, rw)
+    a, b = O.backward(st, dy), O.backward(st, dy, recompute_act=True)
+    for key in ("grad_hidden", "grad_fc2", "grad_gate_up", "grad_routing_weights"):
+        assert torch.equal(a[key], b[key])
