@@ -8,22 +8,31 @@
 // expert e, C_e = A_e * B_e over the rows [offsets[e], offsets[e+1]).
 //
 // MI355X design
-//  * One workgroup = 4 wavefronts computing a BM x BN tile with
-//    v_mfma_f32_32x32x16_bf16 (each wave owns a (BM/WM) x (BN/WN) sub-tile).
-//  * Both operands are staged through LDS in a K-contiguous [row][BK+8]
-//    layout (double-buffered, one barrier per K step). Sources whose K axis
-//    is contiguous are copied with 16-byte vectors; sources whose M/N axis is
-//    contiguous (e.g. gate_up_weight [E, H, 2I], or the rows of the wgrad
-//    operands) are transposed on the way into LDS, 4 K-rows at a time.
+//  * A workgroup of 8 wavefronts (2 per SIMD; 4 for the 128 x 128 tiles)
+//    computes a BM x BN tile with v_mfma_f32_32x32x16_bf16, each wave owning
+//    a (BM / WM) x (BN / WN) sub-tile.
+//  * Operands go global -> LDS with gfx950 LDS-DMA (global_load_lds_dwordx4)
+//    through an NST-stage ring, one barrier per K step. K-contiguous sources
+//    sit in LDS as [rows][BK] with XOR-swizzled 16-byte slots and are read
+//    with ds_read_b128; M/N-contiguous sources (gate_up_weight [E, H, 2I],
+//    the natural down weight, both wgrad operands) keep their natural
+//    [BK][cols] layout, swizzled per 4 K-rows, and are read with the
+//    transposing ds_read_b64_tr_b16. No transposes in HBM or registers.
 //  * Ragged experts: a one-workgroup kernel turns offsets[] into a list of
-//    (expert, first row) M-tiles on the device; the GEMM grid is an upper
-//    bound and surplus workgroups exit at once. Workgroup ids are remapped so
-//    that each XCD (ids congruent mod 8) receives a contiguous range of
-//    tiles, and tiles are grouped GROUP_M-deep along M so that A panels and
-//    B tiles are reused from that XCD's L2.
-//  * FC1 epilogue: the B tile interleaves 32-column groups of gate and up so
-//    every lane holds gate(i, j) and up(i, j) of the same (row, column) and
-//    applies the weighted gated activation before a single bf16 store.
+//    (expert, first row, end row) M-tiles on the device; the GEMM grid is an
+//    upper bound and surplus workgroups exit at once. Workgroup ids are
+//    remapped so that each XCD (ids congruent mod 8) receives a contiguous
+//    range of tiles, grouped GROUP_M-deep along M so that A panels and B
+//    tiles are reused from that XCD's L2. Waves whose rows lie past a
+//    partial tile's end skip their MFMAs.
+//  * FC1 epilogue: the B tile interleaves 32-column groups of gate and up;
+//    the tile is staged in LDS as bf16 gate | up, and each thread turns one
+//    8-column vector of a row into the weighted gated activation (plus the
+//    saved raw FC1 output in bf16, fp16 or fp8 with per-row group scales).
+//  * Weight gradients: deep-K experts use 256 x 256 tiles over the ragged K
+//    (rows), with every expert's tiles spread evenly over the XCDs; small-K
+//    experts use a persistent kernel that streams (tile, K step) stages
+//    through an LDS ring and is bound by writing the gradient.
 #include <stdlib.h>
 #include <string.h>
 
@@ -264,32 +273,19 @@ struct MmaTile {
   // of sub-step kk issue.
   template <class ATile, class BTile, int BK_>
   __device__ void compute(const bf16* As, const bf16* Bs, int wm, int wn, int lane) {
-#ifdef MM_IGLP
-    __builtin_amdgcn_iglp_opt(MM_IGLP);
-#endif
     bf16x8 a[2][MI], b[2][NI];
-#ifdef MM_DIAG_NOA
-#define MM_AFRAG(r0, kk) (bf16x8{})
-#else
-#define MM_AFRAG(r0, kk) ATile::frag(As, r0, kk, lane)
-#endif
-#ifdef MM_DIAG_NOB
-#define MM_BFRAG(r0, kk) (bf16x8{})
-#else
-#define MM_BFRAG(r0, kk) BTile::frag(Bs, r0, kk, lane)
-#endif
 #pragma unroll
-    for (int i = 0; i < MI; ++i) a[0][i] = MM_AFRAG(wm * TM + i * 32, 0);
+    for (int i = 0; i < MI; ++i) a[0][i] = ATile::frag(As, wm * TM + i * 32, 0, lane);
 #pragma unroll
-    for (int j = 0; j < NI; ++j) b[0][j] = MM_BFRAG(wn * TN + j * 32, 0);
+    for (int j = 0; j < NI; ++j) b[0][j] = BTile::frag(Bs, wn * TN + j * 32, 0, lane);
 #pragma unroll
     for (int s = 0; s < BK_ / 16; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
       if (s + 1 < BK_ / 16) {
 #pragma unroll
-        for (int i = 0; i < MI; ++i) a[nxt][i] = MM_AFRAG(wm * TM + i * 32, (s + 1) * 16);
+        for (int i = 0; i < MI; ++i) a[nxt][i] = ATile::frag(As, wm * TM + i * 32, (s + 1) * 16, lane);
 #pragma unroll
-        for (int j = 0; j < NI; ++j) b[nxt][j] = MM_BFRAG(wn * TN + j * 32, (s + 1) * 16);
+        for (int j = 0; j < NI; ++j) b[nxt][j] = BTile::frag(Bs, wn * TN + j * 32, (s + 1) * 16, lane);
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
