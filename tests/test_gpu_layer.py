@@ -79,10 +79,11 @@ def test_routing_plan_and_dispatch_fc1():
     assert_rel(res.fc1_output, gu, 1e-2, "fc1_output")
 
 
-def test_autograd_function_matches_backward():
+@pytest.mark.parametrize("fmt", ["bf16", "fp8"])
+def test_autograd_function_matches_backward(fmt):
     spec = SMALL[0]
     inp = make_inputs(spec, device="cuda", seed=11, weight_scale=0.1)
-    op = _op(spec)
+    op = _op(spec, save_fc1_dtype=fmt)
     x = inp["x"].clone().requires_grad_(True)
     rw = inp["rw"].clone().requires_grad_(True)
     w1 = inp["gate_up"].clone().requires_grad_(True)
@@ -91,7 +92,7 @@ def test_autograd_function_matches_backward():
     out.backward(inp["dy"])
     torch.cuda.synchronize()
     ref_out, st = O.forward(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"].cpu(), w2.detach().cpu(),
-                            inp["rw"].cpu())
+                            inp["rw"].cpu(), save_fc1_dtype=fmt)
     ref = O.backward(st, inp["dy"].cpu())
     assert_rel(out.detach(), ref_out, 2e-2, "out")
     assert_rel(x.grad, ref["grad_hidden"], 2e-2, "dx")
