@@ -151,10 +151,13 @@ __device__ __forceinline__ v4i16 lds_read_tr16(const bf16* p) {
 }
 
 // K-contiguous operand: LDS [ROWS][BK_] (BK_ = 64 or 32). Vector slot s of
-// row r holds source K-vector s ^ swz(r): for 128-byte rows swz = r & 7, for
-// 64-byte rows swz = (r >> 1) & 3, so the 8 rows touched by one pass of a
-// 16-byte fragment read land in distinct banks. Rows outside the tile point
-// at a valid row; their products are never stored.
+// row r holds source K-vector s ^ swz(r). The LDS has 64 four-byte banks, so
+// one pass of a 16-byte fragment read serves 16 lanes = 16 consecutive rows:
+// for 128-byte rows, rows r and r + 1 sit in opposite bank halves and
+// swz = (r >> 1) & 7 separates the 8 rows of each half; for 64-byte rows the
+// row itself selects a quarter and swz = (r >> 2) & 3 separates the rest.
+// (Measured: FC1 bank-conflict cycles 2.7e7 -> 8.7e5.) Rows outside the tile
+// point at a valid row; their products are never stored.
 template <int ROWS, int BK_, int NT = kThreads>
 struct KcTile {
   static constexpr int ELEMS = ROWS * BK_;
@@ -164,7 +167,7 @@ struct KcTile {
   static_assert(PER_WAVE * (NT / 64) == CHUNKS, "chunks/waves mismatch");
   const bf16* ptr[PER_WAVE];
 
-  __device__ static int swz(int r) { return VPR == 8 ? (r & 7) : ((r >> 1) & 3); }
+  __device__ static int swz(int r) { return VPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
 
   template <class RowPtr>
   __device__ void init(RowPtr row_ptr) {
@@ -906,17 +909,6 @@ RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
   return c;
 }
 
-// Pipeline variant of the 256x256 tile: 1 = BK 64 x 2 stages (default,
-// measured faster), 0 = BK 32 x 4 stages (MM_GEMM_PIPE=bk32, for A/B runs).
-int pipe_variant() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("MM_GEMM_PIPE");
-    v = (e && strcmp(e, "bk32") == 0) ? 0 : 1;
-  }
-  return v;
-}
-
 template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
@@ -966,10 +958,8 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   if (c.bm == 256) {
     if (eight_waves())
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
-    else if (pipe_variant() == 1)
-      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
     else
-      launch_rows_cfg<256, 256, 32, 4, BLAYOUT, EPI>(p, max_rows, E, s);
+      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
   } else if (c.bn == 256) {
     if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
       launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
