@@ -373,7 +373,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   grouped_mn(l, num_m, num_n, mt, nt);
   const int4 tile = p.tl->tiles[mt];
   const int e = tile.x, row0 = tile.y, rows = tile.z - tile.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int n0 = nt * BN;
   const bf16* bexp = p.b + static_cast<int64_t>(e) * p.b_se;
