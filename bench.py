@@ -185,6 +185,20 @@ def main():
     roof["kernel"] = "fc1_swiglu (grouped_rows_kernel gated) + tile-list build"
     roof["kernel_ms"] = f1_ms
 
+    # HBM-bound row kernels against the 8 TB/s peak (algorithmic bytes / stage time)
+    R, T, H, I = spec.routes, spec.tokens, spec.hidden, spec.inter
+    bw_bytes = {"combine": 2.0 * R * H + 2.0 * T * H + 4.0 * R}
+    if spec.backward:
+        bw_bytes["combine_bwd"] = 2.0 * R * H + 2.0 * T * H + 4.0 * R + 2.0 * R + 4.0 * R
+        bw_bytes["swiglu_bwd"] = 10.0 * R * I + 6.0 * R
+    bandwidth = {}
+    for name, nbytes in bw_bytes.items():
+        t = stages.get(name)
+        if t:
+            gbs = nbytes / (t * 1e-3) / 1e9
+            bandwidth[name] = {"GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "ms": t}
+    bandwidth["route"] = {"ms": stages.get("route"), "note": "latency-bound (<= 2 MB of tables)"}
+
     cpu = None
     if not args.no_cpu_baseline:
         toks = args.cpu_tokens or {"toy": 512, "e32": 4096, "qwen": 2048, "kimi": 2, "skew": 512}[spec.name]
@@ -215,6 +229,7 @@ def main():
                    "global_batch": spec.tokens, "parallelism": "single GPU, all experts resident"},
         "stages_ms": stages,
         "roofline": roof,
+        "bandwidth_kernels": bandwidth,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
