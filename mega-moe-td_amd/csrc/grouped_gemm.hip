@@ -295,6 +295,14 @@ struct MmaTile {
 #pragma unroll
         for (int j = 0; j < NI; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+      // schedule: each MFMA followed by (up to) two of the next step's LDS
+      // fragment reads, instead of the reads clustered ahead of the MFMAs
+      // (measured -3.5% FC1 time)
+#pragma unroll
+      for (int q = 0; q < MI * NI; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
+      }
     }
   }
 
