@@ -263,3 +263,30 @@ def test_saved_recompute_mode(fmt, monkeypatch):
         ref = O.backward(st, inp["dy"].cpu(), recompute_act=True)
         for name in names:
             assert_rel(g1[name], ref[name], 2e-2, name)
+
+
+def test_backward_function_over_unpacked_weights():
+    """MegaMoEBackwardFunction (reference ops/backward.py:405-455): unpacked
+    fc1_1 / fc1_2 [E, F, H] and fc2 [E, H, F]; gradients flow back to every
+    input in those layouts."""
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=41, weight_scale=0.1)
+    I = spec.inter
+    gu = inp["gate_up"]                                     # [E, H, 2I]
+    fc1_1 = gu[:, :, :I].transpose(1, 2).contiguous().requires_grad_(True)
+    fc1_2 = gu[:, :, I:].transpose(1, 2).contiguous().requires_grad_(True)
+    fc2 = inp["down"].contiguous().requires_grad_(True)     # [E, H, I]
+    x = inp["x"].clone().requires_grad_(True)
+    rw = inp["rw"].clone().requires_grad_(True)
+    out = mega_moe.MegaMoEBackwardFunction.apply(x, rw, inp["selected"], fc1_1, fc1_2, fc2, None, spec.top_k,
+                                                 torch.empty(1, device="cuda"))
+    out.backward(inp["dy"])
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), inp["selected"].cpu(), gu.cpu(), fc2.detach().cpu(), inp["rw"].cpu())
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out.detach(), ref_out, 2e-2, "out")
+    assert_rel(x.grad, ref["grad_hidden"], 2e-2, "dx")
+    assert_rel(rw.grad, ref["grad_routing_weights"], 2e-2, "drw")
+    assert_rel(fc1_1.grad, ref["grad_gate_up"][:, :, :I].transpose(1, 2), 2e-2, "dfc1_1")
+    assert_rel(fc1_2.grad, ref["grad_gate_up"][:, :, I:].transpose(1, 2), 2e-2, "dfc1_2")
+    assert_rel(fc2.grad, ref["grad_fc2"], 2e-2, "dfc2")
