@@ -16,8 +16,12 @@ _WS_CACHE: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
-    """Grow-only per-device byte workspace (reused across calls on one stream)."""
-    key = (str(device), tag)
+    """Grow-only byte workspace per (device, current stream, tag).
+
+    Calls on one stream are ordered, so they can share it; work on another
+    stream gets its own, so concurrent streams never race on a tile list.
+    """
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream, tag)
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
