@@ -89,11 +89,11 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
 
 // Grouped ordering of a (num_m x num_n) tile grid: GROUP_M M-tiles at a time
 // sweep all N tiles, so an A panel and a B tile stay hot in L2.
-__device__ __forceinline__ void grouped_mn(int l, int num_m, int num_n, int& m, int& n) {
-  const int in_group = GROUP_M * num_n;
+__device__ __forceinline__ void grouped_mn(int l, int num_m, int num_n, int& m, int& n, int group_m = GROUP_M) {
+  const int in_group = group_m * num_n;
   const int g = l / in_group;
-  const int first = g * GROUP_M;
-  const int gs = min(num_m - first, GROUP_M);
+  const int first = g * group_m;
+  const int gs = min(num_m - first, group_m);
   const int r = l - g * in_group;
   m = first + r % gs;
   n = r / gs;
@@ -345,6 +345,7 @@ struct RowsArgs {
   bf16* c;
   int64_t ldc;
   const TileList* tl;
+  int group_m;  // M tiles per grouped sweep of the N tiles
   // gated (FC1) epilogue
   const float* w;
   void* fc1_out;   // saved raw gate | up in fc1_fmt (MM_FC1_*), or null
@@ -378,7 +379,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   const int l = xcd_remap(blockIdx.x, num_m * num_n);
   if (l < 0) return;
   int mt, nt;
-  grouped_mn(l, num_m, num_n, mt, nt);
+  grouped_mn(l, num_m, num_n, mt, nt, p.group_m);
   const int4 tile = p.tl->tiles[mt];
   const int e = tile.x, row0 = tile.y, rows = tile.z - tile.y;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -963,6 +964,10 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   const RowsCfg c = pick_rows_cfg(max_rows, E, p.n);
   if (int rc = launch_tiles(offsets, E, c.bm, ws, s)) return rc;
   p.tl = static_cast<const TileList*>(ws);
+  // 128-row tiles (experts averaging < 256 rows, weight-streaming): one
+  // expert's N tiles run together, so its gathered A panel stays in L2
+  // (Kimi-scale: -5% layer time against 8-deep groups)
+  p.group_m = c.bm == 128 ? 1 : GROUP_M;
   if (c.bm == 256) {
     if (eight_waves())
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
