@@ -29,6 +29,21 @@ static inline hipStream_t mm_hip_stream(mm_stream_t s) { return reinterpret_cast
 
 static inline size_t mm_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// ---------------------------------------------------------------- streaming loads
+// 16- / 8-byte loads of data read exactly once (gathered rows of the combine
+// and of the gated-activation backward): the non-temporal hint keeps them
+// from displacing reused lines in L2 (measured: combine 5.3 -> 5.8 TB/s).
+typedef unsigned mm_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned mm_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  const mm_u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const mm_u32x4*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 load_stream8(const void* p) {
+  const mm_u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const mm_u32x2*>(p));
+  return make_uint2(t.x, t.y);
+}
+
 // ---------------------------------------------------------------- bf16
 // Round-to-nearest-even fp32 -> bf16 with gfx950's v_cvt_pk_bf16_f32: equal
 // to torch's float->bfloat16 conversion for every non-NaN input (NaN stays a

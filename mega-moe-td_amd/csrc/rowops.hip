@@ -1,3 +1,4 @@
+#include <stdlib.h>
 // Row-wise bandwidth kernels: dispatch gather, top-k combine, routing-weight
 // gradient gather, gated-activation backward. All are HBM-bound; each
 // wavefront owns one row and moves it with 16-byte vector loads/stores.
@@ -74,9 +75,10 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const uint4* __restri
 // out[t] = bf16(sum_j fp32(y[route_to_send[t*k+j]])), slot order j = 0..k-1.
 // c_split wavefronts share a token row (interleaved passes of 64 * VPL
 // vectors); each lane handles VPL 16-byte vectors per pass and issues the
-// loads of 4 slots for all of them before accumulating, so 4 * VPL row reads
-// are in flight per lane.
-template <int VPL>
+// loads of SLOTS slots for all of them before accumulating, so SLOTS * VPL
+// row reads are in flight per lane (one round trip per pass for top-8).
+// Rows are read once: non-temporal loads.
+template <int VPL, int SLOTS>
 __global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restrict__ y, int64_t ldy_v,
                                                            const int32_t* __restrict__ route_to_send,
                                                            int64_t T, int top_k, int hidden_v,
@@ -95,23 +97,23 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restri
       for (int u = 0; u < VPL; ++u)
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[u][q] = 0.0f;
-      for (int j0 = 0; j0 < top_k; j0 += 4) {
-        uint4 val[4][VPL];
-        int rr[4];
+      for (int j0 = 0; j0 < top_k; j0 += SLOTS) {
+        uint4 val[SLOTS][VPL];
+        int rr[SLOTS];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
+        for (int jj = 0; jj < SLOTS; ++jj) {
           const int j = j0 + jj;
           rr[jj] = __shfl(my_row, j < top_k ? j : 0);
           if (j >= top_k) rr[jj] = -1;
 #pragma unroll
           for (int u = 0; u < VPL; ++u) {
             const int v = v0 + u * 64;
-            val[jj][u] = (rr[jj] >= 0 && v < hidden_v) ? y[static_cast<int64_t>(rr[jj]) * ldy_v + v]
+            val[jj][u] = (rr[jj] >= 0 && v < hidden_v) ? load_stream16(y + static_cast<int64_t>(rr[jj]) * ldy_v + v)
                                                         : make_uint4(0, 0, 0, 0);
           }
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
+        for (int jj = 0; jj < SLOTS; ++jj) {
           if (rr[jj] < 0) continue;
 #pragma unroll
           for (int u = 0; u < VPL; ++u) {
@@ -180,6 +182,12 @@ struct Fc1Row {
   static constexpr int BYTES = FMT == MM_FC1_FP8 ? 8 : 16;  // bytes per 8 values
   typedef typename std::conditional<FMT == MM_FC1_FP8, uint2, uint4>::type Vec;
   __device__ static Vec load(const uint8_t* row, int v) { return reinterpret_cast<const Vec*>(row)[v]; }
+  __device__ static Vec load_stream(const uint8_t* row, int v) {
+    if constexpr (FMT == MM_FC1_FP8)
+      return load_stream8(row + static_cast<int64_t>(v) * BYTES);
+    else
+      return load_stream16(row + static_cast<int64_t>(v) * BYTES);
+  }
   __device__ static Vec zero() {
     if constexpr (FMT == MM_FC1_FP8) return make_uint2(0, 0);
     else return make_uint4(0, 0, 0, 0);
@@ -231,9 +239,9 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
       for (int u = 0; u < 2; ++u) {
         const int v = v0 + 64 * u;
         const bool in = v < inter_v;
-        gv[u] = in ? g_row[v] : make_uint4(0, 0, 0, 0);
-        av[u] = in ? F::load(a_row, v) : F::zero();
-        bv[u] = in ? F::load(b_row, v) : F::zero();
+        gv[u] = in ? load_stream16(g_row + v) : make_uint4(0, 0, 0, 0);
+        av[u] = in ? F::load_stream(a_row, v) : F::zero();
+        bv[u] = in ? F::load_stream(b_row, v) : F::zero();
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -342,7 +350,7 @@ extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_t
   const int64_t passes = (hidden / 8 + 127) / 128;
   const int split = static_cast<int>(std::min<int64_t>(std::min<int64_t>(passes, 4),
                                                         std::max<int64_t>(1, (16384 + num_tokens - 1) / num_tokens)));
-  combine_kernel<2><<<grid_for_rows(num_tokens * split), kThreads, 0, mm_hip_stream(stream)>>>(
+  combine_kernel<2, 8><<<grid_for_rows(num_tokens * split), kThreads, 0, mm_hip_stream(stream)>>>(
       reinterpret_cast<const uint4*>(y), ldy / 8, route_to_send, num_tokens, top_k, hidden / 8,
       reinterpret_cast<uint4*>(out), ldo / 8, split);
   return mm_check_launch("mm_combine");
