@@ -361,7 +361,7 @@ enum { B_KCONTIG = 0, B_NCONTIG = 1 };
 
 // NST-stage ring of LDS buffers: stage s is copied into buffer s % NST while
 // the MFMAs consume stage s - NST + 1; one barrier per K step.
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads>
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, int ACT = 0>
 __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   constexpr int WN = 2, WM = NT / 64 / WN;  // 4 waves: 2x2, 8 waves: 4x2
   using Mma = MmaTile<BM, BN, WM, WN>;
@@ -427,6 +427,18 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   // partial last tile of an expert) skip their MFMAs; their accumulators stay
   // zero and those rows are never stored
   const bool active = wm * Mma::TM < rows;
+  // gated epilogue: each thread's routing weights (rows tid / VPR + i * NT / VPR
+  // of the tile) are fetched now, their latency hidden by the main loop
+  constexpr int EPI_VPR = BN / 16, EPI_IT = EPI == EPI_GATED ? BM * EPI_VPR / NT : 1;
+  float w_pre[EPI_IT];
+  if constexpr (EPI == EPI_GATED) {
+    static_assert(NT % EPI_VPR == 0 && (BM * EPI_VPR) % NT == 0, "epilogue passes");
+#pragma unroll
+    for (int it = 0; it < EPI_IT; ++it) {
+      const int r = threadIdx.x / EPI_VPR + it * (NT / EPI_VPR);
+      w_pre[it] = r < rows ? p.w[row0 + r] : 0.0f;
+    }
+  }
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s)
     if (s < nk) issue(s);
@@ -477,7 +489,10 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
     const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
     // every lane runs every pass (rows past the tile only skip their
     // stores) so that the 16 lanes of a row can reduce the FP8 group amax
-    for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
+    static_assert(VPR == EPI_VPR, "epilogue vector split");
+#pragma unroll
+    for (int it = 0; it < EPI_IT; ++it) {
+      const int idx = threadIdx.x + it * NT;
       const int r = idx / VPR, cv = idx % VPR;
       const bool valid = r < rows;
       const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
@@ -485,13 +500,13 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
       const int64_t row = row0 + r;
       const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
       if (valid) {
-        const float wr = p.w[row];
+        const float wr = w_pre[it];
         uint32_t ow[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float a0 = gated_act(p.act_kind, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
+          const float a0 = gated_act(ACT, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
                                      p.beta, p.lbeta, p.clamp) * wr;
-          const float a1 = gated_act(p.act_kind, __uint_as_float(gw[q] & 0xffff0000u),
+          const float a1 = gated_act(ACT, __uint_as_float(gw[q] & 0xffff0000u),
                                      __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
           ow[q] = pack_bf16x2(a0, a1);
         }
@@ -922,7 +937,16 @@ template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThre
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
-  grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT><<<grid, NT, 0, s>>>(p);
+  if constexpr (EPI == EPI_GATED) {  // activation specialised at compile time
+    if (p.act_kind == MM_ACT_SWIGLU)
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SWIGLU><<<grid, NT, 0, s>>>(p);
+    else if (p.act_kind == MM_ACT_CLAMP_SWIGLU)
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_CLAMP_SWIGLU><<<grid, NT, 0, s>>>(p);
+    else
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SITUGLU><<<grid, NT, 0, s>>>(p);
+  } else {
+    grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT><<<grid, NT, 0, s>>>(p);
+  }
 }
 
 // 8 waves (2 per SIMD) per 256x256 and 128x256 workgroup by default: a
