@@ -274,7 +274,10 @@ struct MmaTile {
 
   // One BK_-deep step; fragments of sub-step kk+16 are read while the MFMAs
   // of sub-step kk issue.
-  template <class ATile, class BTile, int BK_>
+  // TRANS: the MFMA takes its operands swapped, so acc[i][j] holds the
+  // transposed block and lane l has 4 consecutive output columns of row
+  // l % 32 per group of 4 accumulator elements (see acc_col).
+  template <class ATile, class BTile, int BK_, bool TRANS = false>
   __device__ void compute(const bf16* As, const bf16* Bs, int wm, int wn, int lane) {
     bf16x8 a[2][MI], b[2][NI];
 #pragma unroll
@@ -294,7 +297,8 @@ struct MmaTile {
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = TRANS ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[cur][j], a[cur][i], acc[i][j], 0, 0, 0)
+                            : __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
       // schedule: each MFMA followed by (up to) two of the next step's LDS
       // fragment reads, instead of the reads clustered ahead of the MFMAs
       // (measured -3.5% FC1 time)
@@ -309,6 +313,9 @@ struct MmaTile {
   // Tile row of accumulator element r (0..15) of a 32x32 block for `lane`;
   // the column is lane & 31.
   __device__ static int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
+  // TRANS layout: elements 4g .. 4g + 3 of a block sit in row lane % 32 and
+  // columns acc_col(g, lane) .. + 3.
+  __device__ static int acc_col(int g, int lane) { return g * 8 + (lane >> 5) * 4; }
 };
 
 // Epilogue staging: a BM x NC bf16 tile is written to LDS ([BM][NC+8], the
@@ -320,6 +327,10 @@ struct StageOut {
   static constexpr int ELEMS = BM * PITCH;
   __device__ static void put(bf16* lds, int r, int c, float v) {
     reinterpret_cast<uint16_t*>(lds)[r * PITCH + c] = f32_to_bf16_bits(v);
+  }
+  // four consecutive columns c .. c + 3 (c % 4 == 0) of row r: one 8-byte write
+  __device__ static void put4(bf16* lds, int r, int c, float v0, float v1, float v2, float v3) {
+    *reinterpret_cast<uint2*>(lds + r * PITCH + c) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
   }
   // out points at (row 0, column 0) of the tile; ld in elements.
   __device__ static void flush(const bf16* lds, int rows, bf16* out, int64_t ld) {
@@ -448,7 +459,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
       __syncthreads();
       if (kt + NST - 1 < nk) issue(kt + NST - 1);
       const bf16* cur = smem + (kt % NST) * STAGE;
-      mma.template compute<ATile, BTile, BK_>(cur, cur + ATile::ELEMS, wm, wn, lane);
+      mma.template compute<ATile, BTile, BK_, true>(cur, cur + ATile::ELEMS, wm, wn, lane);
     }
   } else {  // same copies and barriers, no MFMAs
     for (int kt = 0; kt < nk; ++kt) {
@@ -459,17 +470,19 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   }
   __syncthreads();
 
-  // ---- epilogue (LDS-staged, 16-byte stores)
-  const int col = lane & 31;
+  // ---- epilogue (LDS-staged, 16-byte stores). The accumulators are
+  // transposed (compute<..., true>): each lane stages 4 consecutive columns
+  // of its row with one 8-byte write.
+  const int trow = wm * Mma::TM + (lane & 31);
   if constexpr (EPI == EPI_STORE) {
 #pragma unroll
     for (int i = 0; i < Mma::MI; ++i)
 #pragma unroll
       for (int j = 0; j < Mma::NI; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + j * 32 + col,
-                   mma.acc[i][j][r]);
+        for (int g = 0; g < 4; ++g)
+          Out::put4(smem, trow + i * 32, wn * Mma::TN + j * 32 + Mma::acc_col(g, lane), mma.acc[i][j][4 * g],
+                    mma.acc[i][j][4 * g + 1], mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
     Out::flush(smem, rows, p.c + static_cast<int64_t>(row0) * p.ldc + n0, p.ldc);
   } else {
     // Stage bf16(gate) in LDS columns [0, BN/2) and bf16(up) in [BN/2, BN)
@@ -481,9 +494,11 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
 #pragma unroll
       for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane),
-                   (jj & 1) * (BN / 2) + wn * (Mma::TN / 2) + (jj >> 1) * 32 + col, mma.acc[i][jj][r]);
+        for (int g = 0; g < 4; ++g)
+          Out::put4(smem, trow + i * 32,
+                    (jj & 1) * (BN / 2) + wn * (Mma::TN / 2) + (jj >> 1) * 32 + Mma::acc_col(g, lane),
+                    mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1], mma.acc[i][jj][4 * g + 2],
+                    mma.acc[i][jj][4 * g + 3]);
     __syncthreads();
     constexpr int VPR = BN / 16;  // 8-column vectors per output row
     const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
