@@ -690,9 +690,8 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
       issue(kt + 1);
       if (kt + 2 < nk) fetch_rows(kt + 2);
     }
-    mma.template compute<PTile, QTile, BK_>(cur, cur + PTile::ELEMS, wm, wn, lane);
+    mma.template compute<PTile, QTile, BK_, true>(cur, cur + PTile::ELEMS, wm, wn, lane);
   }
-  const int col = lane & 31;
   bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + static_cast<int64_t>(t1) * BM * a.n2 + t2 * BN;
   if constexpr (DIRECT) {
     // stage the tile unpadded in the (now idle) stage buffers, 16-byte
@@ -705,11 +704,12 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
 #pragma unroll
       for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tr = wm * Mma::TM + i * 32 + Mma::acc_row(r, lane);
-          const int tc = wn * Mma::TN + jj * 32 + col;
-          reinterpret_cast<uint16_t*>(smem)[tr * BN + ((((tc >> 3) ^ (tr & 7)) << 3) | (tc & 7))] =
-              f32_to_bf16_bits(mma.acc[i][jj][r]);
+        for (int g = 0; g < 4; ++g) {  // transposed accumulators: 4 consecutive columns per lane
+          const int tr = wm * Mma::TM + i * 32 + (lane & 31);
+          const int tc = wn * Mma::TN + jj * 32 + Mma::acc_col(g, lane);
+          *reinterpret_cast<uint2*>(smem + tr * BN + ((((tc >> 3) ^ (tr & 7)) << 3) | (tc & 7))) =
+              make_uint2(pack_bf16x2(mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1]),
+                         pack_bf16x2(mma.acc[i][jj][4 * g + 2], mma.acc[i][jj][4 * g + 3]));
         }
     __syncthreads();
     for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
@@ -724,9 +724,10 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
 #pragma unroll
       for (int jj = 0; jj < Mma::NI; ++jj)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Out::put(smem, wm * Mma::TM + i * 32 + Mma::acc_row(r, lane), wn * Mma::TN + jj * 32 + col,
-                   mma.acc[i][jj][r]);
+        for (int g = 0; g < 4; ++g)  // transposed accumulators: 4 consecutive columns per lane
+          Out::put4(smem, wm * Mma::TM + i * 32 + (lane & 31), wn * Mma::TN + jj * 32 + Mma::acc_col(g, lane),
+                    mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1], mma.acc[i][jj][4 * g + 2],
+                    mma.acc[i][jj][4 * g + 3]);
     Out::flush(smem, BM, out, a.n2);
   }
 }
