@@ -1014,10 +1014,22 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     else
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
   } else if (c.bn == 256) {
-    if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
-      launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
-    else
-      launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
+    // Weight streaming with N-contiguous weights (FC1, FC2 of small
+    // experts): 512-wide tiles halve the tile count and with it the per-tile
+    // prologue / epilogue (Kimi-scale FC1 -6%, FC2 -10%; neutral to +2% for
+    // the K-contiguous dgrads, which keep 256). The FP8 save needs 256-wide
+    // tiles (its scale groups are tile halves).
+    bool wide = false;
+    if constexpr (BLAYOUT == B_NCONTIG) {
+      wide = p.n % 512 == 0 && !(EPI == EPI_GATED && p.fc1_out && p.fc1_fmt == MM_FC1_FP8);
+      if (wide) launch_rows_cfg<128, 512, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+    }
+    if (!wide) {
+      if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
+        launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+      else
+        launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
+    }
   } else {
     launch_rows_cfg<128, 128, 64, 4, BLAYOUT, EPI>(p, max_rows, E, s);
   }
