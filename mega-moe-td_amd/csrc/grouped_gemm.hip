@@ -739,6 +739,14 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
 // output write dominates.
 __device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
 
+// Two consecutive int32 at a wave-uniform address, loaded through the scalar
+// cache (completion tracked by lgkmcnt, not vmcnt).
+__device__ __forceinline__ int2 scalar_load_i32x2(const int32_t* p) {
+  uint64_t v;
+  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return make_int2(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(v >> 32));
+}
+
 // wait until at most n (rounded down to a multiple of STEP) vector-memory
 // ops of this wave are outstanding; n is wave-uniform
 template <int MAXN, int STEP>
@@ -779,9 +787,13 @@ __device__ __forceinline__ void wait_vmcnt_atmost(int n) {
 struct TileCursor {
   int e, t, ks, nk, kr, r0;
   bool valid;
+  // offsets[e], offsets[e + 1] come from one scalar load: the compiler emits
+  // a vector load for them otherwise and follows it with vmcnt(0), which
+  // drains every in-flight stage copy and tile store at each new expert
   __device__ void load_expert(const int32_t* offsets, int rows_cap) {
-    r0 = __builtin_amdgcn_readfirstlane(min(offsets[e], rows_cap));
-    kr = __builtin_amdgcn_readfirstlane(min(offsets[e + 1], rows_cap)) - r0;
+    const int2 o = scalar_load_i32x2(offsets + __builtin_amdgcn_readfirstlane(e));
+    r0 = min(o.x, rows_cap);
+    kr = min(o.y, rows_cap) - r0;
     nk = kr > 0 ? (kr + 31) / 32 : 1;  // an expert without rows still writes its zero tiles
   }
   __device__ void skip_empty(int c, int per_e, int E, const int32_t* offsets, int rows_cap) {
