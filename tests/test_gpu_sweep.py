@@ -1,0 +1,88 @@
+"""Seeded sweep of layer shapes (GPU): forward and the five-stage backward
+against the CPU oracle, over shapes the fixed cases do not reach.
+
+Each case draws tokens, hidden / intermediate sizes (multiples of 128),
+expert count, top-k, routing (softmax top-k, Zipf-skewed, uniform distinct),
+the activation, the saved FC1 format and the down-weight layout, and drops a
+few routes, as the reference's layer suite does with its drop cases
+(tests/layer/test_moe_suite.py:371-470). Rows per expert range from 0 to
+several thousand, so the 128- and 256-row tile paths, the 512-wide tiles of
+the weight-streaming GEMMs, both weight-gradient kernels and empty experts
+are all reached. Tolerances are the reference's (tests/_numeric.py:27-68).
+"""
+
+import random
+
+import pytest
+import torch
+
+import mega_moe
+from mega_moe.bench_configs import CaseSpec, make_inputs
+from oracle import moe_oracle as O
+from tests._numeric import GRAD_ATOL, GRAD_RTOL, OUTPUT_ATOL, OUTPUT_RTOL, assert_rel, cmp_grad
+
+pytestmark = pytest.mark.gpu
+
+ACTS = {
+    "swiglu": dict(situ_beta=1.0, situ_linear_beta=None, clamp_limit=7.0),
+    "clamp_swiglu": dict(situ_beta=1.0, situ_linear_beta=None, clamp_limit=0.05),
+    "situglu": dict(situ_beta=2.0, situ_linear_beta=3.0, clamp_limit=7.0),
+}
+
+
+def _case(i):
+    """Configuration i (deterministic)."""
+    r = random.Random(1000 + i)
+    E = r.choice([1, 2, 3, 5, 8, 16, 40])
+    k = r.choice([k for k in (1, 2, 4, 8) if k <= E])
+    H = r.choice([128, 256, 384, 512, 1024])
+    inter = r.choice([128, 256, 384, 512])
+    # bounded oracle cost: routes * H * I <= ~4e8
+    t_max = max(1, int(4e8 / (k * H * inter)))
+    T = r.choice([t for t in (1, 3, 17, 64, 200, 700, 1500) if t <= t_max] or [1])
+    routing = r.choice(["softmax_topk", "zipf", "uniform_distinct"])
+    act = r.choice(list(ACTS))
+    fmt = r.choice(["bf16", "bf16", "fp16", "fp8"])
+    contiguous_down = r.random() < 0.5
+    return dict(T=T, H=H, I=inter, E=E, k=k, routing=routing, act=act, fmt=fmt, contiguous_down=contiguous_down,
+                seed=r.randrange(1 << 30))
+
+
+CASES = [_case(i) for i in range(40)]
+
+
+def _id(c):
+    return (f"T{c['T']}-H{c['H']}-I{c['I']}-E{c['E']}-k{c['k']}-{c['routing']}-{c['act']}-{c['fmt']}"
+            f"-{'cdown' if c['contiguous_down'] else 'tdown'}")
+
+
+@pytest.mark.parametrize("c", CASES, ids=_id)
+def test_layer_sweep(c):
+    spec = CaseSpec("sweep", c["T"], c["H"], c["I"], c["E"], c["k"], c["routing"], True)
+    inp = make_inputs(spec, device="cuda", seed=c["seed"], weight_scale=0.1)
+    sel = inp["selected"].clone()
+    g = torch.Generator().manual_seed(c["seed"])
+    drops = torch.rand(sel.shape, generator=g) < 0.05
+    bad = torch.where(torch.rand(sel.shape, generator=g) < 0.5, -1, c["E"] + 3).to(torch.int32)
+    sel = torch.where(drops.cuda(), bad.cuda(), sel).contiguous()
+    down = inp["down"].contiguous() if c["contiguous_down"] else inp["down"]
+    kw = ACTS[c["act"]]
+    # the configured FC2 N tile must divide H (the reference's tile check)
+    tiles = dict(fc2_gemm_block_size_n=128) if c["H"] % 256 else {}
+    cfg = mega_moe.MoEForwardConfig(activation=c["act"], save_fc1_dtype=c["fmt"], **tiles, **kw)
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=c["T"], hidden_size=c["H"], top_k=c["k"],
+                                  num_experts=c["E"], config=cfg)
+    print(f"sweep case {_id(c)}", flush=True)
+    out, saved = op.forward(inp["x"], sel, inp["gate_up"], down, inp["rw"], return_saved=True)
+    grads = mega_moe.moe_backward_triton(saved, inp["dy"], peer_mem=None)
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), sel.cpu(), inp["gate_up"].cpu(), down.cpu(), inp["rw"].cpu(),
+                            activation=c["act"], save_fc1_dtype=c["fmt"], **kw)
+    ref = O.backward(st, inp["dy"].cpu())
+    assert_rel(out, ref_out, 2e-2, "output")
+    torch.testing.assert_close(out.float().cpu(), ref_out.float(), rtol=OUTPUT_RTOL, atol=OUTPUT_ATOL)
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
+        assert_rel(grads[name], ref[name], 2e-2, name)
+        assert cmp_grad(grads[name], ref[name], GRAD_RTOL, GRAD_ATOL) == 0, name
+    dropped = drops.cuda()
+    assert torch.all(grads["grad_routing_weights"][dropped] == 0)
