@@ -839,8 +839,24 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
   constexpr int SPT = HALVES * SUB / 8 / 64;              // stores per lane per tile
   __shared__ __attribute__((aligned(1024))) bf16 smem[NST * STAGE + (NT / 64) * SUB];
   const int x = blockIdx.x % kXcds, c = blockIdx.x / kXcds, nc = gridDim.x / kXcds;
-  const int t2n = a.n2 / BN;
-  const int per_e = (a.n1 / BM) * t2n;
+  const int t1n = a.n1 / BM, t2n = a.n2 / BN;
+  const int per_e = t1n * t2n;
+  // Tile t of an expert -> (t1, t2): the dimension with more tiles varies
+  // fastest, so the workgroups of an XCD write tiles spread along it and
+  // share the operand block of the other dimension. Measured on the
+  // Kimi-scale gradients against the other order: dW1 (28 x 16 tiles)
+  // 11.4 -> 10.3 ms, dW2 (28 x 8) 5.55 -> 5.3 ms; a transposed 8 x 28 shape
+  // runs 4.8 ms in this order and 6.3 ms in the other.
+  const bool t1_fast = t1n >= t2n;
+  auto tile_of = [&](int t, int& t1, int& t2) {
+    if (t1_fast) {
+      t1 = t % t1n;
+      t2 = t / t1n;
+    } else {
+      t1 = t / t2n;
+      t2 = t % t2n;
+    }
+  };
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -851,7 +867,8 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
   lc = cc;
   auto issue = [&](const TileCursor& q, int buf) {
     bf16* dst = smem + buf * STAGE;
-    const int t1 = q.t / t2n, t2 = q.t % t2n;
+    int t1, t2;
+    tile_of(q.t, t1, t2);
     const int kb = q.ks * BKS;
     const bf16* prow0 = a.p + static_cast<int64_t>(q.r0 + kb) * a.ldp + t1 * BM;
     const bf16* qrow0 = a.q + static_cast<int64_t>(q.r0 + kb) * a.ldq + t2 * BN;
@@ -905,7 +922,8 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
     for (int ss = 0; ss < nsub; ++ss)
       mma.template compute<QTile, PTile, 16>(pb + PTile::ELEMS + ss * 16 * BN, pb + ss * 16 * BM, wm, wn, lane);
     if (cc.ks == cc.nk - 1) {
-      const int t1 = cc.t / t2n, t2 = cc.t % t2n;
+      int t1, t2;
+      tile_of(cc.t, t1, t2);
       bf16* out = a.c + static_cast<int64_t>(cc.e) * a.n1 * a.n2 +
                   static_cast<int64_t>(t1 * BM + wn * Mma::TN) * a.n2 + t2 * BN + wm * Mma::TM;
 #pragma unroll
