@@ -30,6 +30,7 @@ import torch.distributed
 
 from ..config import MoEForwardConfig
 from ..runtime.routing import MoERoutingPlan, RouteTables, plan_from_tables, route
+from ._saved import MoESaved
 from ..runtime.timing import NULL_TIMER
 from . import _kernels as K
 
@@ -354,13 +355,13 @@ class FusedMoEForward(torch.nn.Module):
             tm.end()
         if not return_saved:
             return out
-        saved = dict(
+        saved = MoESaved(
             batch_size=num_tokens, hidden_dim=self.hidden_size, ffn_dim=inter, num_experts=self.num_experts,
             experts_per_rank=self.experts_per_rank, topk=self.top_k, world_size=1, ep_rank=0,
             ep_group=self.ep_group, total_routes=num_routes,
             activation=self.activation, situ_beta=self.situ_beta, situ_linear_beta=self.situ_linear_beta,
             clamp_limit=self.clamp_limit,
-            hidden_states=hidden_states, selected_experts=selected_experts,
+            hidden_states=hidden_states, selected_experts=selected_experts, routing_weights=routing_weights,
             gate_up_weight=gate_up_weight, down_weight=down_weight, fc2=down_weight,
             _owner_token=id(self._routing_owner_token), _routing_generation=self._routing_generation,
             _single_kernel_snapshot=False, _stage_timer=self.stage_timer,
