@@ -91,3 +91,35 @@ def test_backward_requires_saved_activations():
         mega_moe.moe_backward_triton({}, torch.zeros(1, 1))
     with pytest.raises(NotImplementedError):
         mega_moe.moe_backward_triton({"fc1_output": None}, torch.zeros(1, 1), grad_transport=object())
+
+
+def test_saved_dict_derives_reference_keys_on_cpu():
+    """MoESaved: reference contract keys as closed forms of the stored tables."""
+    from mega_moe.ops._saved import MoESaved
+
+    E, k, F, H = 5, 2, 128, 256
+    sel = torch.tensor([[0, 3], [3, 1], [-1, 0], [4, 3], [1, 9]], dtype=torch.int32)
+    flat = sel.reshape(-1).long()
+    valid = (flat >= 0) & (flat < E)
+    order = torch.argsort(flat.float(), stable=True)
+    send_route = order[valid[order]].int()
+    counts = torch.bincount(flat[valid], minlength=E).int()
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = counts.cumsum(0)
+    w1 = torch.randn(E, H, 2 * F).bfloat16()
+    x = torch.randn(5, H).bfloat16()
+    s = MoESaved(num_experts=E, experts_per_rank=E, ffn_dim=F, split_size_cum_per_expert=offsets,
+                 expert_counts=counts, send_route_indices=send_route, send_token_indices=send_route // k,
+                 gate_up_weight=w1, hidden_states=x)
+    n = int(valid.sum())
+    assert "meta_tile_num" in s and "nonexistent" not in s and s.get("nonexistent") is None
+    assert s["total_recv"] == s["M"] == n and s["splits_send_list"] == [n]
+    assert s["meta_expert_ids"].tolist() == [e for e in range(E) if counts[e] > 0]  # every count < 64
+    assert s["num_tiles_total"].tolist() == [int((counts > 0).sum())]
+    assert torch.equal(s["sort_idxs"], send_route.long())
+    assert torch.equal(s["sort_idxs"][s["inv_sort"]], torch.sort(send_route.long()).values)
+    assert torch.equal(s["recv_hidden_sorted"], x[send_route.long() // k])
+    assert s["fc1_combined"].shape == (E, 2 * F, H) and s["fc1_1"].data_ptr() == w1.data_ptr()
+    assert torch.equal(s["recv_counts_by_source_expert"], counts.view(1, E))
+    with pytest.raises(KeyError):
+        s["not_a_key"]
