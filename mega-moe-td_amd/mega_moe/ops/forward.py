@@ -216,6 +216,33 @@ class FusedMoEForward(torch.nn.Module):
             raise RuntimeError(
                 "FusedMoEForward is single-stream; recreate the operator for a different caller stream")
 
+    # ------------------------------------------------------------ lifecycle
+    def sync(self):
+        """Wait for the work queued on the current device (reference ops/forward.py:284-285)."""
+        torch.cuda.synchronize()
+
+    def finalize(self):
+        """Drain queued work before the caller releases the operator's tensors
+        (reference ops/forward.py:287-300). One GPU holds no symmetric memory
+        or transport streams, so draining the device is all there is to do."""
+        torch.cuda.synchronize()
+
+    def read_last_forward_phase_timing(self):
+        """Mean per-stage milliseconds of the passes recorded by the attached
+        ``runtime.timing.StageTimer`` (``op.stage_timer``), the HIP-event
+        counterpart of the reference's single-kernel phase stamps
+        (ops/forward.py:1555-1570). Synchronises. Raises ``RuntimeError``
+        when no timer is attached, as the reference does before any timed
+        forward has run."""
+        if self.stage_timer is None:
+            raise RuntimeError("no stage timer is attached to this operator; set op.stage_timer = StageTimer()")
+        return self.stage_timer.summary()
+
+    def lend_replica_weight_tables_for_grad(self, *, experts_to_copy_cpu=None):
+        """MoonEP replica tables (reference ops/forward.py:1322) do not exist
+        on one GPU: expert parallelism and MoonEP are not built."""
+        raise NotImplementedError("MoonEP replica weight tables are not built (one GPU, no expert parallelism)")
+
     def _route(self, selected_experts, routing_weights) -> RouteTables:
         num_routes = selected_experts.numel()
         need = int(K._lib.load().mm_route_workspace_bytes(num_routes, self.experts_per_rank))

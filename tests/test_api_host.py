@@ -123,3 +123,12 @@ def test_saved_dict_derives_reference_keys_on_cpu():
     assert torch.equal(s["recv_counts_by_source_expert"], counts.view(1, E))
     with pytest.raises(KeyError):
         s["not_a_key"]
+
+
+def test_operator_timing_and_moonep_entry_points():
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=4, hidden_size=256, top_k=2, num_experts=4)
+    with pytest.raises(RuntimeError, match="stage timer"):
+        op.read_last_forward_phase_timing()
+    with pytest.raises(NotImplementedError, match="MoonEP"):
+        op.lend_replica_weight_tables_for_grad()
+    assert callable(op.sync) and callable(op.finalize)

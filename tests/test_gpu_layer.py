@@ -290,3 +290,18 @@ def test_backward_function_over_unpacked_weights():
     assert_rel(fc1_1.grad, ref["grad_gate_up"][:, :, :I].transpose(1, 2), 2e-2, "dfc1_1")
     assert_rel(fc1_2.grad, ref["grad_gate_up"][:, :, I:].transpose(1, 2), 2e-2, "dfc1_2")
     assert_rel(fc2.grad, ref["grad_fc2"], 2e-2, "dfc2")
+
+
+def test_stage_timing_sync_finalize():
+    from mega_moe.runtime.timing import StageTimer
+
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=9)
+    op = _op(spec)
+    op.stage_timer = StageTimer()
+    out = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
+    op.sync()
+    t = op.read_last_forward_phase_timing()
+    assert {"route", "fc1_swiglu", "fc2", "combine"} <= set(t) and all(v > 0 for v in t.values())
+    op.finalize()
+    assert out.shape == inp["x"].shape
