@@ -156,14 +156,16 @@ def test_grouped_wgrad(kind, gather, tiling, monkeypatch):
             assert torch.count_nonzero(c[e]) == 0
 
 
+@pytest.mark.parametrize("shape", [(512, 1280), (1280, 512)], ids=["n2_tiles_more", "n1_tiles_more"])
 @pytest.mark.parametrize("tiling", ["wide", "tile"])
-def test_grouped_wgrad_many_experts_both_gathered(tiling, monkeypatch):
+def test_grouped_wgrad_many_experts_both_gathered(tiling, shape, monkeypatch):
     """Small-K regime with many experts: rows 0..140 per expert (zero-row
     experts, a last K stage of <= 16 rows, multi-stage K, one 300-row
     expert), both operands gathered (permuted into the workspace first)."""
     from mega_moe.ops import _kernels as K
     monkeypatch.setenv("MM_WGRAD_KERNEL", tiling)
-    E, N1, N2 = 21, 512, 1280
+    E = 21
+    N1, N2 = shape  # both tile walks of the small-K kernel (more tiles along n1 or along n2)
     rng = np.random.default_rng(11)
     cnt = rng.integers(0, 141, size=E)
     cnt[[2, 9]] = 0
