@@ -1063,11 +1063,13 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     // experts): 512-wide tiles halve the tile count and with it the per-tile
     // prologue / epilogue (Kimi-scale FC1 -6%, FC2 -10%; neutral to +2% for
     // the K-contiguous dgrads, which keep 256). The FP8 save needs 256-wide
-    // tiles (its scale groups are tile halves).
+    // tiles (its scale groups are tile halves). BK 32 x 4 stages (4 x 40 KiB)
+    // keeps three stages of weight in flight per CU instead of one 80 KiB
+    // stage (Kimi-scale FC1 -4%, FC2 -6% against BK 64 x 2).
     bool wide = false;
     if constexpr (BLAYOUT == B_NCONTIG) {
       wide = p.n % 512 == 0 && !(EPI == EPI_GATED && p.fc1_out && p.fc1_fmt == MM_FC1_FP8);
-      if (wide) launch_rows_cfg<128, 512, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+      if (wide) launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
     }
     if (!wide) {
       if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
