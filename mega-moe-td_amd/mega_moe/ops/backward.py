@@ -52,6 +52,8 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     x = hidden_states if hidden_states is not None else saved["hidden_states"]
     if dy.shape != (T, H):
         raise ValueError(f"dy must have shape {(T, H)}, got {tuple(dy.shape)}")
+    if x.shape != (T, H) or x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError(f"hidden_states must be a contiguous bf16 tensor of shape {(T, H)}")
     dy = dy.to(torch.bfloat16).contiguous()
     act_kw = dict(activation=saved["activation"], situ_beta=saved["situ_beta"],
                   situ_linear_beta=saved["situ_linear_beta"], clamp_limit=saved["clamp_limit"])

@@ -132,3 +132,20 @@ def test_operator_timing_and_moonep_entry_points():
     with pytest.raises(NotImplementedError, match="MoonEP"):
         op.lend_replica_weight_tables_for_grad()
     assert callable(op.sync) and callable(op.finalize)
+
+
+def test_backward_validates_dy_and_hidden_states_on_cpu():
+    """Host-side checks of moe_backward_triton run before any launch."""
+    T, H = 4, 256
+    saved = dict(batch_size=T, topk=2, hidden_dim=H, ffn_dim=128, total_routes=8, fc1_output=torch.empty(0),
+                 gate_up_weight=None, down_weight=None, split_size_cum_per_expert=None,
+                 send_token_indices=None, route_to_send=None, hidden_states=torch.zeros(T, H).bfloat16())
+    with pytest.raises(ValueError, match="dy must have shape"):
+        mega_moe.moe_backward_triton(saved, torch.zeros(T + 1, H), peer_mem=None)
+    with pytest.raises(ValueError, match="hidden_states must be"):
+        mega_moe.moe_backward_triton(saved, torch.zeros(T, H), peer_mem=None,
+                                     hidden_states=torch.zeros(T, H))  # fp32
+    with pytest.raises(ValueError, match="missing fc1_output"):
+        mega_moe.moe_backward_triton({}, torch.zeros(T, H), peer_mem=None)
+    with pytest.raises(NotImplementedError, match="MoonEP"):
+        mega_moe.moe_backward_triton(saved, torch.zeros(T, H), peer_mem=None, grad_transport=object())
