@@ -559,11 +559,15 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
           store_out16(fo, make_uint4(gh[0], gh[1], gh[2], gh[3]));
           store_out16(fo + p.inter, make_uint4(uh[0], uh[1], uh[2], uh[3]));
         }
-      } else {
-        // FP8: one scale per row per BN/2 = MM_FC1_SCALE_GROUP columns of gate
-        // (and of up), i.e. per row of this tile; the row's 16 lanes reduce
-        // the amax of |bf16 value| with xor shuffles
-        static_assert(BN / 2 == MM_FC1_SCALE_GROUP || EPI != EPI_GATED || BN != 256, "scale group = tile half");
+      } else if constexpr ((BN / 2) % MM_FC1_SCALE_GROUP == 0) {
+        // FP8: one scale per row per MM_FC1_SCALE_GROUP columns of gate (and
+        // of up); a tile row holds BN / 2 of them, i.e. one or two groups.
+        // The group's 16 consecutive lanes reduce the amax of |bf16 value|
+        // with xor shuffles. (Narrower tiles never see FP8: mm_fc1_swiglu
+        // requires inter % MM_FC1_SCALE_GROUP == 0 for it, which selects
+        // 256- or 512-wide tiles.)
+        constexpr int GV = MM_FC1_SCALE_GROUP / 8;  // lanes per scale group
+        static_assert(VPR % GV == 0, "scale groups tile the row");
         float ga = 0.0f, ua = 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
           ua = fmaxf(ua, fmaxf(fabsf(__uint_as_float(uw[q] << 16)), fabsf(__uint_as_float(uw[q] & 0xffff0000u))));
         }
 #pragma unroll
-        for (int off = 1; off < VPR; off <<= 1) {
+        for (int off = 1; off < GV; off <<= 1) {
           ga = fmaxf(ga, __shfl_xor(ga, off));
           ua = fmaxf(ua, __shfl_xor(ua, off));
         }
@@ -591,9 +595,9 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
           uint8_t* fo = static_cast<uint8_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
           store_out8(fo, make_uint2(gq[0], gq[1]));
           store_out8(fo + p.inter, make_uint2(uq[0], uq[1]));
-          if (cv == 0) {
+          if (cv % GV == 0) {
             const int groups = p.inter / MM_FC1_SCALE_GROUP;
-            float* sc = p.fc1_scale + row * (2 * groups) + nt;
+            float* sc = p.fc1_scale + row * (2 * groups) + (jbase + cv * 8) / MM_FC1_SCALE_GROUP;
             sc[0] = gs / kFp8Max;
             sc[groups] = us / kFp8Max;
           }
@@ -1062,13 +1066,12 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     // Weight streaming with N-contiguous weights (FC1, FC2 of small
     // experts): 512-wide tiles halve the tile count and with it the per-tile
     // prologue / epilogue (Kimi-scale FC1 -6%, FC2 -10%; neutral to +2% for
-    // the K-contiguous dgrads, which keep 256). The FP8 save needs 256-wide
-    // tiles (its scale groups are tile halves). BK 32 x 4 stages (4 x 40 KiB)
+    // the K-contiguous dgrads, which keep 256). BK 32 x 4 stages (4 x 40 KiB)
     // keeps three stages of weight in flight per CU instead of one 80 KiB
     // stage (Kimi-scale FC1 -4%, FC2 -6% against BK 64 x 2).
     bool wide = false;
     if constexpr (BLAYOUT == B_NCONTIG) {
-      wide = p.n % 512 == 0 && !(EPI == EPI_GATED && p.fc1_out && p.fc1_fmt == MM_FC1_FP8);
+      wide = p.n % 512 == 0;
       if (wide) launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
     }
     if (!wide) {
