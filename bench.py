@@ -1,17 +1,21 @@
 """Benchmark of the MI355X Mega-MoE layer (one GPU).
 
-    python bench.py [--config e32|qwen|kimi|skew|toy] [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--config kimi|qwen|skew|e32|toy] [--steps K] [--warmup W] [--gpus 1]
+
+The default is the headline configuration: the Kimi-scale layer (T=4096,
+H=7168, I=2048, E=896, top-16), forward + backward.
 
 A step is one pass of the layer over one batch of synthetic input resident in
 HBM: forward (routing -> FC1+gated act -> FC2 -> combine) and, for configs
 that train, the five-stage backward. ``value`` is the layer's algorithmic
 throughput in TFLOP/s (6RHI forward, +12RHI backward) over the timed steps;
 ``ms_per_step`` is the layer latency. ``roofline`` reports the dominant
-kernel (FC1 grouped GEMM + fused activation) against the MFMA bf16 dense
-peak or, for the weight-streaming Kimi shape, against HBM bandwidth, from
-HIP events recorded on the launch stream inside the timed region.
-``cpu_baseline`` times the CPU restatement of the reference's Torch path
-(oracle/moe_oracle.py) on a bounded token sample of the same configuration.
+GEMM stage (the longest) against the MFMA bf16 dense peak or, for the
+weight-streaming Kimi shape, against HBM bandwidth, from HIP events recorded
+on the launch stream inside the timed region, plus the whole step against
+its floor. ``cpu_baseline`` times the CPU restatement of the reference's
+Torch path (oracle/moe_oracle.py) on a bounded sample of the same
+configuration.
 """
 
 from __future__ import annotations
@@ -20,6 +24,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -35,75 +40,124 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="e32")
+    ap.add_argument("--config", default="kimi", help="toy | e32 | qwen | kimi | skew (default: kimi fwd+bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--save-fc1-dtype", default="bf16", choices=("bf16", "fp16", "fp8"),
                     help="saved FC1 format of the training configs (MoEForwardConfig.save_fc1_dtype)")
-    ap.add_argument("--cpu-tokens", type=int, default=0, help="token sample for the CPU baseline (0 = auto)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
-def fc1_algorithmic(spec, save_fc1: bool):
-    """(flops, bytes) of one FC1+activation launch."""
+def stage_work(spec, save_fc1: bool) -> dict:
+    """Algorithmic (flops, HBM bytes) of one launch of each GEMM stage.
+
+    Bytes count every operand once: the weight table (2 bytes per element),
+    the gathered or expert-major activation rows read, the rows written, and
+    the saved FC1 output when the forward keeps it.
+    """
     R, H, I, E = spec.routes, spec.hidden, spec.inter, spec.experts
-    flops = 4.0 * R * H * I
-    byts = 2.0 * E * H * 2 * I + 2.0 * R * H + 2.0 * R * I + 4.0 * R + (4.0 * R * I if save_fc1 else 0.0)
-    return flops, byts
+    w1, w2 = 2.0 * E * H * 2 * I, 2.0 * E * H * I
+    return {
+        "fc1_swiglu": (4.0 * R * H * I, w1 + 2.0 * R * H + 2.0 * R * I + 4.0 * R + (4.0 * R * I if save_fc1 else 0.0)),
+        "fc2": (2.0 * R * H * I, w2 + 2.0 * R * I + 2.0 * R * H),
+        "fc2_dgrad": (2.0 * R * H * I, w2 + 2.0 * R * H + 2.0 * R * I),
+        "fc2_wgrad": (2.0 * R * H * I, w2 + 2.0 * R * H + 2.0 * R * I),
+        "fc1_dgrad": (4.0 * R * H * I, w1 + 4.0 * R * I + 2.0 * R * H),
+        "fc1_wgrad": (4.0 * R * H * I, w1 + 2.0 * R * H + 4.0 * R * I),
+    }
 
 
-def cpu_inputs(spec, tokens: int, seed: int = 99):
-    """CPU inputs for a token sample: the sample's routing over all E experts,
-    with weights materialised only for the experts the sample touches
-    (renumbered densely), so the per-token CPU work equals the full layer's."""
+# kernels behind each stage (the stage's HIP-event time also holds the
+# tile-list build, and for the weight gradients the operand permute)
+STAGE_KERNELS = {
+    "fc1_swiglu": "grouped_rows_kernel (gated epilogue)",
+    "fc2": "grouped_rows_kernel",
+    "fc2_dgrad": "grouped_rows_kernel (gathered dy rows)",
+    "fc1_dgrad": "grouped_rows_kernel (K-contiguous gate_up)",
+    "fc2_wgrad": "wgrad_persist_kernel / grouped_wgrad_kernel",
+    "fc1_wgrad": "wgrad_persist_kernel / grouped_wgrad_kernel",
+}
+
+# CPU-baseline sample per config: (tokens, experts). Where the layer's experts
+# are spread evenly, the sample is an expert shard with the same rows per
+# expert (Kimi: 1/32 of the experts and of the tokens, 73 rows per expert as
+# in the full layer); Skew keeps all 32 experts so the Zipf skew is preserved.
+CPU_SAMPLE = {"toy": (512, 8), "e32": (1024, 8), "qwen": (1024, 16), "kimi": (128, 28), "skew": (2048, 32)}
+
+
+def cpu_inputs(spec, tokens: int, experts: int, seed: int = 99):
+    """Seeded CPU inputs of the sample: same H, I, top-k and routing rule as the
+    configuration, over ``experts`` experts and ``tokens`` tokens."""
     import torch
 
     from mega_moe.bench_configs import CaseSpec, make_routing
 
-    s = CaseSpec(spec.name, tokens, spec.hidden, spec.inter, spec.experts, spec.top_k, spec.routing,
+    s = CaseSpec(spec.name, tokens, spec.hidden, spec.inter, experts, spec.top_k, spec.routing,
                  spec.backward, spec.dtype, spec.zipf_s)
     gen = torch.Generator().manual_seed(seed)
     sel, rw = make_routing(s, gen)
-    used = torch.unique(sel)
-    remap = torch.full((spec.experts,), -1, dtype=torch.int32)
-    remap[used.long()] = torch.arange(used.numel(), dtype=torch.int32)
-    sel = remap[sel.long()]
-    U, H, I = used.numel(), spec.hidden, spec.inter
-    bf = torch.bfloat16
-    x = torch.randn(tokens, H, generator=gen).to(bf)
-    dy = torch.randn(tokens, H, generator=gen).to(bf)
-    gate_up = (torch.randn(U, H, 2 * I, generator=gen) * 0.02).to(bf)
-    down = (torch.randn(U, I, H, generator=gen) * 0.02).to(bf).transpose(1, 2)
-    return dict(x=x, selected=sel, rw=rw, gate_up=gate_up, down=down, dy=dy), U
+    H, I = spec.hidden, spec.inter
+    dt = torch.float32 if spec.dtype == "fp32" else torch.bfloat16
+    x = torch.randn(tokens, H, generator=gen).to(dt)
+    dy = torch.randn(tokens, H, generator=gen).to(dt)
+    gate_up = torch.empty(experts, H, 2 * I, dtype=dt)
+    down = torch.empty(experts, I, H, dtype=dt)
+    for e in range(experts):
+        gate_up[e] = torch.randn(H, 2 * I, generator=gen) * 0.02
+        down[e] = torch.randn(I, H, generator=gen) * 0.02
+    return dict(x=x, selected=sel, rw=rw, gate_up=gate_up, down=down.transpose(1, 2), dy=dy)
 
 
-def cpu_baseline(spec, tokens: int):
-    """Time the CPU restatement of the reference's Torch layer on a token sample."""
+def _cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(spec):
+    """Time the CPU restatement of the reference's Torch layer on a sample:
+    1 warm-up, then the median of 3 runs (toy: 10), GEMMs in the config's
+    dtype (bf16 operands, fp32 accumulation; fp32 for the toy config)."""
     import torch
 
     sys.path.insert(0, ROOT)
     from oracle import moe_oracle as O
 
-    threads = torch.get_num_threads()
-    inp, used = cpu_inputs(spec, tokens)
-    times = []
-    for _ in range(2):
+    tokens, experts = CPU_SAMPLE[spec.name]
+    inp = cpu_inputs(spec, tokens, experts)
+    mm = torch.float32 if spec.dtype == "fp32" else torch.bfloat16
+
+    def run():
         t0 = time.perf_counter()
-        out, st = O.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
+        out, st = O.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], matmul_dtype=mm)
         if spec.backward:
             O.backward(st, inp["dy"])
-        times.append(time.perf_counter() - t0)
-    t = min(times)
-    flops = (6.0 + (12.0 if spec.backward else 0.0)) * tokens * spec.top_k * spec.hidden * spec.inter
+        return time.perf_counter() - t0
+
+    run()
+    t = statistics.median(run() for _ in range(10 if spec.name == "toy" else 3))
+    flops_per_route = (6.0 + (12.0 if spec.backward else 0.0)) * spec.hidden * spec.inter
+    rate = flops_per_route * tokens * spec.top_k / t
     return {
-        "value": flops / t / 1e12,
+        "value": rate / 1e12,
         "unit": "TFLOP/s",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
+        "host_cpus": os.cpu_count(),
+        "cpu_model": _cpu_model(),
         "kind": "port",
-        "sample": f"{spec.name} layer {'fwd+bwd' if spec.backward else 'fwd'} on {tokens} of {spec.tokens} tokens "
-                  f"({used} experts touched, full H={spec.hidden}/I={spec.inter}), per-expert fp32 matmul loop "
-                  f"with bf16 rounding, best of 2: {t * 1e3:.0f} ms",
+        "ms_sample": t * 1e3,
+        "ms_full_layer_at_this_rate": flops_per_route * spec.routes / rate * 1e3,
+        "sample": f"{spec.name} layer {'fwd+bwd' if spec.backward else 'fwd'} on {tokens} tokens x {experts} "
+                  f"experts (full: {spec.tokens} x {spec.experts}; same H={spec.hidden}, I={spec.inter}, "
+                  f"top-{spec.top_k}, routing rule), oracle per-expert loop with {str(mm).split('.')[-1]} GEMMs, "
+                  f"1 warm-up + median of {10 if spec.name == 'toy' else 3}: {t * 1e3:.0f} ms; the full-layer "
+                  f"figure scales that rate to the layer's flops, no NPU 256-row M padding",
     }
 
 
@@ -167,23 +221,40 @@ def main():
 
     flops = spec.fwd_flops() + (spec.bwd_flops() if spec.backward else 0.0)
     value = flops / (ms * 1e-3) / 1e12
-    f1_flops, f1_bytes = fc1_algorithmic(spec, save_fc1=spec.backward)
-    f1_ms = stages.get("fc1_swiglu", float("nan"))
+    # dominant GEMM stage (longest HIP-event time) against its roofline:
+    # HBM for the weight-streaming Kimi shape, MFMA for the others
+    work = stage_work(spec, save_fc1=spec.backward)
     weight_bound = spec.name == "kimi"
+    gemm = {}
+    for name, (fl, by) in work.items():
+        t = stages.get(name)
+        if t:
+            gemm[name] = {"ms": t, "TFLOP/s": fl / (t * 1e-3) / 1e12, "GB/s": by / (t * 1e-3) / 1e9,
+                          "mfma_frac": fl / (t * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                          "hbm_frac": by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    dom = max(gemm, key=lambda n: gemm[n]["ms"])
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{spec.name}.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("fc1_swiglu_bytes")
+        traffic = json.load(open(tpath)).get(f"{dom}_bytes")
     if weight_bound:
-        ach = f1_bytes / (f1_ms * 1e-3) / 1e9
+        ach = gemm[dom]["GB/s"]
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS,
                 "traffic": traffic}
     else:
-        ach = f1_flops / (f1_ms * 1e-3) / 1e12
+        ach = gemm[dom]["TFLOP/s"]
         roof = {"bound": "mfma", "achieved": ach, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": ach / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic}
-    roof["kernel"] = "fc1_swiglu (grouped_rows_kernel gated) + tile-list build"
-    roof["kernel_ms"] = f1_ms
+    roof["stage"] = dom
+    roof["kernel"] = STAGE_KERNELS[dom]
+    roof["kernel_ms"] = gemm[dom]["ms"]
+    roof["algorithmic"] = {"flops": work[dom][0], "bytes": work[dom][1]}
+    # whole step against its floor: max(GEMM flops at the MFMA peak, weight
+    # bytes at the HBM peak: read once forward; read and written once backward)
+    w_bytes = spec.weight_bytes() * (3.0 if spec.backward else 1.0)
+    floor_ms = max(flops / (MFMA_BF16_PEAK_TFLOPS * 1e12), w_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
+    roof["step_floor_ms"] = floor_ms
+    roof["step_frac"] = floor_ms / ms
 
     # HBM-bound row kernels against the 8 TB/s peak (algorithmic bytes / stage time)
     R, T, H, I = spec.routes, spec.tokens, spec.hidden, spec.inter
@@ -201,10 +272,9 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        toks = args.cpu_tokens or {"toy": 512, "e32": 4096, "qwen": 2048, "kimi": 2, "skew": 512}[spec.name]
-        print(f"[bench] cpu baseline on {toks} tokens", file=sys.stderr, flush=True)
+        print(f"[bench] cpu baseline on {CPU_SAMPLE[spec.name]} (tokens, experts)", file=sys.stderr, flush=True)
         try:
-            cpu = cpu_baseline(spec, toks)
+            cpu = cpu_baseline(spec)
         except Exception as exc:  # reported, never fatal for the GPU measurement
             cpu = {"value": None, "unit": "TFLOP/s", "cores": None, "kind": "port", "sample": f"failed: {exc}"}
 
@@ -229,6 +299,7 @@ def main():
                    "global_batch": spec.tokens, "parallelism": "single GPU, all experts resident"},
         "stages_ms": stages,
         "roofline": roof,
+        "gemm_stages": gemm,
         "bandwidth_kernels": bandwidth,
         "cpu_baseline": cpu,
     }

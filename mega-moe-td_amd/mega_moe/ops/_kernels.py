@@ -12,26 +12,64 @@ import torch
 
 from .. import _lib
 
-_WS_CACHE: dict = {}
+class WorkspacePool:
+    """Byte workspaces per (device, stream, tag) that never move under a
+    captured graph.
 
-
-def workspace(device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
-    """Grow-only byte workspace per (device, current stream, tag).
-
-    Calls on one stream are ordered, so they can share it; work on another
-    stream gets its own, so concurrent streams never race on a tile list.
+    Calls on one stream are ordered, so they share a workspace; work on
+    another stream gets its own, so concurrent streams never race on a tile
+    list. A workspace that a larger call outgrows is retired, not freed: a
+    HIP graph captured earlier keeps its address baked in, and the retired
+    buffer stays valid for that graph's replays until ``release()``.
+    ``FusedMoEForward`` owns one pool sized for its ``max_tokens_per_rank`` at
+    the first forward, so its own calls never grow it; the module pool serves
+    direct calls of these wrappers.
     """
-    key = (str(device), torch.cuda.current_stream(device).cuda_stream, tag)
-    ws = _WS_CACHE.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _WS_CACHE[key] = ws
-    return ws
+
+    def __init__(self):
+        self._live: dict = {}
+        self._retired: list = []
+
+    def get(self, device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
+        key = (str(device), torch.cuda.current_stream(device).cuda_stream, tag)
+        ws = self._live.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                self._retired.append(ws)
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._live[key] = ws
+        return ws
+
+    def nbytes(self) -> int:
+        return sum(t.numel() for t in self._live.values()) + sum(t.numel() for t in self._retired)
+
+    def release(self):
+        """Drop every workspace (no graph captured over them may replay after this)."""
+        self._live.clear()
+        self._retired.clear()
 
 
-def _gemm_ws(device, max_rows: int, num_experts: int) -> torch.Tensor:
-    need = int(_lib.load().mm_gemm_workspace_bytes(max_rows, num_experts))
-    return workspace(device, need, "gemm")
+_POOL = WorkspacePool()
+
+
+def workspace(device: torch.device, nbytes: int, tag: str, pool: WorkspacePool | None = None) -> torch.Tensor:
+    return (pool or _POOL).get(device, nbytes, tag)
+
+
+def gemm_workspace_bytes(max_rows: int, num_experts: int) -> int:
+    return int(_lib.load().mm_gemm_workspace_bytes(max_rows, num_experts))
+
+
+def route_workspace_bytes(num_routes: int, num_experts: int) -> int:
+    return int(_lib.load().mm_route_workspace_bytes(num_routes, num_experts))
+
+
+def wgrad_workspace_bytes(max_rows: int, num_experts: int, n1: int, n2: int) -> int:
+    return int(_lib.load().mm_wgrad_workspace_bytes(max_rows, num_experts, n1, n2))
+
+
+def _gemm_ws(device, max_rows: int, num_experts: int, pool=None) -> torch.Tensor:
+    return workspace(device, gemm_workspace_bytes(max_rows, num_experts), "gemm", pool)
 
 
 def _check_bf16(name: str, t: torch.Tensor):
@@ -63,7 +101,7 @@ def fc1_format_of(t: torch.Tensor) -> str:
 
 
 def fc1_swiglu(x, send_token, w1, offsets, weight_perm, max_rows: int, activation: str, situ_beta: float,
-               situ_linear_beta, clamp_limit: float, save_fc1: bool, fc1_dtype: str = "bf16"):
+               situ_linear_beta, clamp_limit: float, save_fc1: bool, fc1_dtype: str = "bf16", pool=None):
     """FC1 grouped GEMM + weighted gated activation.
 
     Returns (act [rows, I] bf16, fc1_output [rows, 2I] in ``fc1_dtype`` | None,
@@ -85,7 +123,7 @@ def fc1_swiglu(x, send_token, w1, offsets, weight_perm, max_rows: int, activatio
         if inter % _lib.FC1_SCALE_GROUP:
             raise ValueError(f"fp8 fc1 save needs ffn % {_lib.FC1_SCALE_GROUP} == 0, got {inter}")
         fc1_scale = torch.empty(max_rows, two_inter // _lib.FC1_SCALE_GROUP, dtype=torch.float32, device=dev)
-    ws = _gemm_ws(dev, max_rows, num_experts)
+    ws = _gemm_ws(dev, max_rows, num_experts, pool)
     lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
     _lib.call("mm_fc1_swiglu", _lib.ptr(x), x.stride(0), _lib.ptr(send_token), _lib.ptr(w1), _lib.ptr(offsets),
               _lib.ptr(weight_perm), num_experts, max_rows, hidden, inter, _lib.ACT_KINDS[activation],
@@ -94,7 +132,8 @@ def fc1_swiglu(x, send_token, w1, offsets, weight_perm, max_rows: int, activatio
     return act, fc1_out, fc1_scale
 
 
-def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_rows: int, n: int, k: int):
+def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_rows: int, n: int, k: int,
+                 pool=None):
     """c[i, :] = a[row(i), :] @ B_e for expert-major rows; B_e(k, n) = b[e*se + n*sn + k*sk]."""
     _check_bf16("a", a)
     _check_bf16("b", b)
@@ -102,15 +141,19 @@ def grouped_gemm(a, a_rows, b, b_se: int, b_sn: int, b_sk: int, offsets, max_row
         raise ValueError("grouped_gemm: a must be [*, K] with unit column stride")
     num_experts = offsets.numel() - 1
     c = torch.empty(max_rows, n, dtype=torch.bfloat16, device=a.device)
-    ws = _gemm_ws(a.device, max_rows, num_experts)
+    ws = _gemm_ws(a.device, max_rows, num_experts, pool)
     _lib.call("mm_grouped_gemm", _lib.ptr(a), a.stride(0), _lib.ptr(a_rows), _lib.ptr(b), b_se, b_sn, b_sk,
               _lib.ptr(offsets), num_experts, max_rows, n, k, _lib.ptr(c), c.stride(0), _lib.ptr(ws), ws.numel(),
               _lib.stream_of(a.device))
     return c
 
 
-def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int | None = None) -> torch.Tensor:
-    """c[e] = P_e^T Q_e over each expert's rows -> [E, n1, n2] bf16."""
+def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int | None = None, pool=None,
+                  ws_rows: int | None = None) -> torch.Tensor:
+    """c[e] = P_e^T Q_e over each expert's rows -> [E, n1, n2] bf16.
+
+    ``ws_rows`` (>= max_rows) sizes the workspace, so a pool sized once for an
+    operator's capacity is reused by smaller calls."""
     _check_bf16("p", p)
     _check_bf16("q", q)
     if p.stride(1) != 1 or q.stride(1) != 1 or p.shape[1] != n1 or q.shape[1] != n2:
@@ -119,8 +162,8 @@ def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int
     if max_rows is None:
         max_rows = q.shape[0] if q_rows is None else q_rows.shape[0]
     c = torch.empty(num_experts, n1, n2, dtype=torch.bfloat16, device=p.device)
-    need = int(_lib.load().mm_wgrad_workspace_bytes(max_rows, num_experts, n1, n2))
-    ws = workspace(p.device, need, "wgrad") if need and (p_rows is not None or q_rows is not None) else None
+    need = wgrad_workspace_bytes(max(max_rows, ws_rows or 0), num_experts, n1, n2)
+    ws = workspace(p.device, need, "wgrad", pool) if need and (p_rows is not None or q_rows is not None) else None
     _lib.call("mm_grouped_wgrad", _lib.ptr(p), p.stride(0), _lib.ptr(p_rows), _lib.ptr(q), q.stride(0),
               _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), _lib.ptr(ws),
               0 if ws is None else ws.numel(), _lib.stream_of(p.device))

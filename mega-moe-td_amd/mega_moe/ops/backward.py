@@ -37,6 +37,8 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     """
     if grad_transport is not None:
         raise NotImplementedError("MoonEP replica gradient transport is not built")
+    if saved.get("batch_size") == 0:
+        return _empty_batch_grads(saved, dy)
     if "fc1_output" not in saved:
         raise ValueError("saved is missing fc1_output; run the forward with return_saved=True")
     T = saved["batch_size"]
@@ -59,10 +61,12 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
                   situ_linear_beta=saved["situ_linear_beta"], clamp_limit=saved["clamp_limit"])
 
     tm = saved.get("_stage_timer") or NULL_TIMER
+    pool = saved.get("_workspaces")
+    ws_rows = saved.get("_max_routes") or R
     # step 1: FC2 dgrad, B_e(k=h, n=f) = down[e, h, f]
     tm.begin("fc2_dgrad")
     se, sh, sf = w2.stride()
-    grad_act = K.grouped_gemm(dy, send_token, w2, se, sf, sh, offsets, R, inter, H)
+    grad_act = K.grouped_gemm(dy, send_token, w2, se, sf, sh, offsets, R, inter, H, pool=pool)
     tm.end()
     # step 2: gated-activation backward
     tm.begin("swiglu_bwd")
@@ -84,11 +88,11 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
                           **act_kw)
         tm.end()
     tm.begin("fc2_wgrad")
-    grad_fc2 = K.grouped_wgrad(dy, send_token, act, None, offsets, H, inter)
+    grad_fc2 = K.grouped_wgrad(dy, send_token, act, None, offsets, H, inter, pool=pool, ws_rows=ws_rows)
     tm.end()
     # step 4: FC1 dgrad, B_e(k=j, n=h) = W1[e, h, j]; top-k reduce; gate gather
     tm.begin("fc1_dgrad")
-    dx = K.grouped_gemm(dab, None, w1, w1.stride(0), w1.stride(1), 1, offsets, R, H, 2 * inter)
+    dx = K.grouped_gemm(dab, None, w1, w1.stride(0), w1.stride(1), 1, offsets, R, H, 2 * inter, pool=pool)
     tm.end()
     tm.begin("combine_bwd")
     grad_hidden = K.combine(dx, r2s, T, k)
@@ -96,9 +100,13 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     tm.end()
     # step 5: FC1 wgrad in the packed layout  dW1[e][h, j] = sum_i x[tok(i), h] dAB[i, j]
     tm.begin("fc1_wgrad")
-    grad_gate_up = K.grouped_wgrad(x, send_token, dab, None, offsets, H, 2 * inter)
+    grad_gate_up = K.grouped_wgrad(x, send_token, dab, None, offsets, H, 2 * inter, pool=pool, ws_rows=ws_rows)
     tm.end()
 
+    return _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter)
+
+
+def _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter):
     grad_fc1 = grad_gate_up.transpose(1, 2)  # [E, 2F, H] view
     return dict(
         grad_hidden=grad_hidden,
@@ -112,6 +120,21 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
         grad_gate=dscale,
         grad_fc1=grad_fc1,
     )
+
+
+def _empty_batch_grads(saved, dy):
+    """Gradients of a zero-token batch: empty input gradients and all-zero
+    weight gradients (no expert received a row)."""
+    H, inter, k = saved["hidden_dim"], saved["ffn_dim"], saved["topk"]
+    if tuple(dy.shape) != (0, H):
+        raise ValueError(f"dy must have shape {(0, H)}, got {tuple(dy.shape)}")
+    w1 = saved["gate_up_weight"]
+    dev, bf = w1.device, torch.bfloat16
+    E = w1.shape[0]
+    return _grad_dict(torch.empty(0, H, dtype=bf, device=dev), torch.empty(0, k, dtype=torch.float32, device=dev),
+                      torch.zeros(E, H, inter, dtype=bf, device=dev), torch.zeros(E, H, 2 * inter, dtype=bf, device=dev),
+                      torch.empty(0, inter, dtype=bf, device=dev), torch.empty(0, 2 * inter, dtype=bf, device=dev),
+                      torch.empty(0, dtype=bf, device=dev), inter)
 
 
 class MegaMoEBackwardFunction(torch.autograd.Function):

@@ -34,6 +34,10 @@ from ._saved import MoESaved
 from ..runtime.timing import NULL_TIMER
 from . import _kernels as K
 
+# Device-kernel limits (csrc/routing.hip kMaxExperts, csrc/rowops.hip combine slots).
+MAX_EXPERTS = 1024
+MAX_TOP_K = 64
+
 
 @dataclass
 class DispatchFC1Result:
@@ -73,6 +77,11 @@ class FusedMoEForward(torch.nn.Module):
             raise ValueError("top_k must be positive")
         if num_experts <= 0:
             raise ValueError("num_experts must be positive")
+        if num_experts > MAX_EXPERTS:
+            raise ValueError(f"num_experts must be <= {MAX_EXPERTS} (the routing kernel's per-expert tables), "
+                             f"got {num_experts}")
+        if top_k > MAX_TOP_K:
+            raise ValueError(f"top_k must be <= {MAX_TOP_K} (the combine kernel's slot limit), got {top_k}")
         if config is not None and not isinstance(config, MoEForwardConfig):
             raise TypeError("config must be a MoEForwardConfig instance or None")
 
@@ -118,6 +127,11 @@ class FusedMoEForward(torch.nn.Module):
         self._device = None
         # optional runtime.timing.StageTimer: HIP events between stages
         self.stage_timer = None
+        # operator-owned workspaces (routing scratch, tile lists, weight-gradient
+        # operand staging), sized for max_tokens_per_rank at the first forward so
+        # that they never move afterwards (a captured graph keeps their addresses)
+        self._workspaces = K.WorkspacePool()
+        self._ws_ready = False
 
     # ------------------------------------------------------------ validation
     def _check_device(self, t: torch.Tensor, name: str):
@@ -222,10 +236,13 @@ class FusedMoEForward(torch.nn.Module):
         torch.cuda.synchronize()
 
     def finalize(self):
-        """Drain queued work before the caller releases the operator's tensors
-        (reference ops/forward.py:287-300). One GPU holds no symmetric memory
-        or transport streams, so draining the device is all there is to do."""
+        """Drain queued work and release the operator's workspaces (reference
+        ops/forward.py:287-300). One GPU holds no symmetric memory or
+        transport streams; graphs captured over this operator must not be
+        replayed after finalize()."""
         torch.cuda.synchronize()
+        self._workspaces.release()
+        self._ws_ready = False
 
     def read_last_forward_phase_timing(self):
         """Mean per-stage milliseconds of the passes recorded by the attached
@@ -243,10 +260,24 @@ class FusedMoEForward(torch.nn.Module):
         on one GPU: expert parallelism and MoonEP are not built."""
         raise NotImplementedError("MoonEP replica weight tables are not built (one GPU, no expert parallelism)")
 
+    @property
+    def max_routes(self) -> int:
+        return self.max_tokens_per_rank * self.top_k
+
+    def _reserve_workspaces(self, device):
+        """Size the routing and tile-list workspaces for the operator's capacity."""
+        if self._ws_ready:
+            return
+        R, E = self.max_routes, self.experts_per_rank
+        self._workspaces.get(device, K.route_workspace_bytes(R, E), "route")
+        self._workspaces.get(device, K.gemm_workspace_bytes(R, E), "gemm")
+        self._ws_ready = True
+
     def _route(self, selected_experts, routing_weights) -> RouteTables:
+        self._reserve_workspaces(selected_experts.device)
         num_routes = selected_experts.numel()
-        need = int(K._lib.load().mm_route_workspace_bytes(num_routes, self.experts_per_rank))
-        ws = K.workspace(selected_experts.device, need, "route")
+        need = K.route_workspace_bytes(num_routes, self.experts_per_rank)
+        ws = self._workspaces.get(selected_experts.device, need, "route")
         return route(selected_experts, self.experts_per_rank, routing_weights, ws)
 
     # ------------------------------------------------------------ routing
@@ -319,7 +350,7 @@ class FusedMoEForward(torch.nn.Module):
         dispatched = K.permute(hidden_states, routing_plan.send_token_indices, offsets, m)
         if m:
             gu = K.grouped_gemm(dispatched, None, fc1_weight, fc1_weight.stride(0), 1, fc1_weight.stride(1),
-                                offsets, m, output_size, self.hidden_size)
+                                offsets, m, output_size, self.hidden_size, pool=self._workspaces)
         else:
             gu = torch.empty(0, output_size, dtype=torch.bfloat16, device=hidden_states.device)
         if fc1_output is not None:
@@ -370,12 +401,12 @@ class FusedMoEForward(torch.nn.Module):
             act, fc1_out, fc1_scale = K.fc1_swiglu(
                 hidden_states, tables.send_token, gate_up_weight, tables.offsets, tables.weight_perm, num_routes,
                 self.activation, self.situ_beta, self.situ_linear_beta, self.clamp_limit, save_fc1=return_saved,
-                fc1_dtype=self.config.save_fc1_dtype)
+                fc1_dtype=self.config.save_fc1_dtype, pool=self._workspaces)
             tm.end()
             tm.begin("fc2")
             se, sh, sf = down_weight.stride()
             y = K.grouped_gemm(act, None, down_weight, se, sh, sf, tables.offsets, num_routes, self.hidden_size,
-                               inter)
+                               inter, pool=self._workspaces)
             tm.end()
             tm.begin("combine")
             out = K.combine(y, tables.route_to_send, num_tokens, self.top_k)
@@ -392,6 +423,7 @@ class FusedMoEForward(torch.nn.Module):
             gate_up_weight=gate_up_weight, down_weight=down_weight, fc2=down_weight,
             _owner_token=id(self._routing_owner_token), _routing_generation=self._routing_generation,
             _single_kernel_snapshot=False, _stage_timer=self.stage_timer,
+            _workspaces=self._workspaces, _max_routes=self.max_routes,
         )
         if tables is not None:
             saved.update(

@@ -49,6 +49,13 @@ def bf16(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.bfloat16).to(torch.float32)
 
 
+def _mm(a: torch.Tensor, b: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
+    """a @ b with operands in ``dtype`` (fp32: the checker; bf16: bf16 GEMMs
+    with fp32 accumulation, as the reference's Torch path runs them), fp32
+    result."""
+    return (a.to(dtype) @ b.to(dtype)).float()
+
+
 # --------------------------------------------------------------------- routing
 def route(selected: np.ndarray, num_experts: int, top_k: int) -> dict:
     """Stable expert-major routing tables (runtime/routing.py:621-671)."""
@@ -165,8 +172,11 @@ def dequantize_fc1(stored: torch.Tensor, scale=None) -> torch.Tensor:
 
 # --------------------------------------------------------------------- forward
 def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, situ_linear_beta=None,
-            clamp_limit=7.0, save_fc1_dtype="bf16"):
+            clamp_limit=7.0, save_fc1_dtype="bf16", matmul_dtype=torch.float32):
     """Layer forward on CPU.
+
+    ``matmul_dtype`` bf16 runs the GEMMs on bf16 operands (the timed CPU
+    baseline); every GEMM output is rounded to bf16 either way.
 
     x [T, H] bf16; selected [T, k] int32; gate_up [E, H, 2I] bf16;
     down [E, H, I] bf16 (any strides); rw [T, k] fp32.
@@ -181,8 +191,9 @@ def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, 
     send_route = torch.from_numpy(tb["send_route"]).long()
     offsets = tb["offsets"]
     xf = x.float().cpu()
-    w1 = gate_up.float().cpu()
-    w2 = down.float().cpu()
+    mm = matmul_dtype
+    w1 = gate_up.cpu().to(mm)
+    w2 = down.cpu().to(mm)
     wp = rw.float().cpu().reshape(-1)[send_route]
     M = send_route.numel()
     gate = torch.empty(M, inter)
@@ -193,7 +204,7 @@ def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, 
         a, b = int(offsets[e]), int(offsets[e + 1])
         if a == b:
             continue
-        gu = xp[a:b] @ w1[e]
+        gu = _mm(xp[a:b], w1[e], mm)
         gate[a:b] = bf16(gu[:, :inter])
         up[a:b] = bf16(gu[:, inter:])
     act = bf16(gated_act(gate, up, activation, situ_beta, situ_linear_beta, clamp_limit) * wp[:, None])
@@ -201,7 +212,7 @@ def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, 
         a, b = int(offsets[e]), int(offsets[e + 1])
         if a == b:
             continue
-        y[a:b] = bf16(act[a:b] @ w2[e].T)
+        y[a:b] = bf16(_mm(act[a:b], w2[e].T, mm))
     r2s = torch.from_numpy(tb["route_to_send"]).long().view(T, k)
     out = torch.zeros(T, H)
     for j in range(k):
@@ -211,7 +222,7 @@ def forward(x, selected, gate_up, down, rw, activation="swiglu", situ_beta=1.0, 
     fc1_saved, fc1_scale = quantize_fc1(torch.cat([gate, up], dim=1), save_fc1_dtype)
     state = dict(tables=tb, x=xf, w1=w1, w2=w2, wp=wp, gate=gate, up=up, act=act, y=y, T=T, k=k, E=E,
                  inter=inter, activation=activation, situ_beta=situ_beta, situ_linear_beta=situ_linear_beta,
-                 clamp_limit=clamp_limit, fc1_output=fc1_saved, fc1_output_scale=fc1_scale)
+                 clamp_limit=clamp_limit, fc1_output=fc1_saved, fc1_output_scale=fc1_scale, mm=mm)
     return out.to(torch.bfloat16), state
 
 
@@ -253,6 +264,7 @@ def backward(state, dy, recompute_act=False):
     offsets = tb["offsets"]
     send_token = torch.from_numpy(tb["send_token"]).long()
     w1, w2 = state["w1"], state["w2"]
+    mm = state.get("mm", torch.float32)
     dyf = dy.float().cpu()
     H = dyf.shape[1]
     gco = bf16(dyf)[send_token]                                   # step 1a
@@ -261,7 +273,7 @@ def backward(state, dy, recompute_act=False):
     for e in range(E):                                            # step 1b
         a, b = int(offsets[e]), int(offsets[e + 1])
         if a < b:
-            grad_act[a:b] = bf16(gco[a:b] @ w2[e])
+            grad_act[a:b] = bf16(_mm(gco[a:b], w2[e], mm))
     scale = bf16(state["wp"])[:, None]                            # step 2
     gu = dequantize_fc1(state["fc1_output"], state.get("fc1_output_scale"))  # the saved (maybe narrowed) FC1
     act_a, dact, v, dv = gated_act_grad(gu[:, :inter], gu[:, inter:], state["activation"], state["situ_beta"],
@@ -282,9 +294,9 @@ def backward(state, dy, recompute_act=False):
         a, b = int(offsets[e]), int(offsets[e + 1])
         if a == b:
             continue
-        grad_fc2[e] = bf16(gco[a:b].T @ act_saved[a:b])
-        dx[a:b] = bf16(dab[a:b] @ w1[e].T)                        # step 4a
-        grad_gate_up[e] = bf16(xp[a:b].T @ dab[a:b])              # step 5
+        grad_fc2[e] = bf16(_mm(gco[a:b].T, act_saved[a:b], mm))
+        dx[a:b] = bf16(_mm(dab[a:b], w1[e].T, mm))                      # step 4a
+        grad_gate_up[e] = bf16(_mm(xp[a:b].T, dab[a:b], mm))            # step 5
     r2s = torch.from_numpy(tb["route_to_send"]).long().view(T, k)
     grad_hidden = torch.zeros(T, H)                               # step 4b
     grad_rw = torch.zeros(T, k)
@@ -302,6 +314,110 @@ def backward(state, dy, recompute_act=False):
         grad_fc1_output=dab,
         grad_gate=dscale,
     )
+
+
+# --------------------------------------------------------------------- sampled backward
+def _expert_rows(xr, dyr, wr, w1e, w2e, activation, situ_beta, situ_linear_beta, clamp_limit):
+    """Forward and backward quantities of one expert's rows (same rounding
+    points as ``forward`` / ``backward``).
+
+    xr, dyr [n, H] fp32 (bf16 values); wr [n] fp32 routing weights;
+    w1e [H, 2I], w2e [H, I] fp32. Every GEMM here has the operand shapes the
+    per-expert loops of ``forward`` / ``backward`` use for the same rows, so
+    for an expert's complete row set the results are bit-identical to theirs.
+    """
+    inter = w1e.shape[1] // 2
+    gu = xr @ w1e
+    gate, up = bf16(gu[:, :inter]), bf16(gu[:, inter:])
+    act = bf16(gated_act(gate, up, activation, situ_beta, situ_linear_beta, clamp_limit) * wr[:, None])
+    y = bf16(act @ w2e.T)
+    gco = bf16(dyr)
+    grad_act = bf16(gco @ w2e)                                        # step 1
+    scale = bf16(wr)[:, None]                                         # step 2
+    act_a, dact, v, dv = gated_act_grad(gate, up, activation, situ_beta, situ_linear_beta, clamp_limit)
+    dab = bf16(torch.cat([grad_act * dact * v * scale, grad_act * act_a * dv * scale], dim=1))
+    dscale = bf16((act_a * v * grad_act).sum(dim=1))
+    dx = bf16(dab @ w1e.T)                                            # step 4a
+    return dict(act=act, y=y, gco=gco, dab=dab, dscale=dscale, dx=dx)
+
+
+def _act_kw(kw):
+    return (kw.get("activation", "swiglu"), kw.get("situ_beta", 1.0), kw.get("situ_linear_beta"),
+            kw.get("clamp_limit", 7.0))
+
+
+def backward_tokens(x, selected, gate_up, down, rw, dy, tokens, **act_kw):
+    """Layer output and input gradients for a subset of tokens only.
+
+    Restates forward steps FC1 -> act -> FC2 -> combine and backward steps
+    1, 2 and 4 (tests/_moe_baselines.py:96-226: gco gather, FC2 dgrad,
+    gated-activation backward, FC1 dgrad, top-k reduce in slot order,
+    grad_routing_weights = dscale of the route's row, 0 if dropped) for the
+    routes of ``tokens``; the routes of one expert are evaluated together, so
+    each expert's weights are read once. Inputs may live on any device; the
+    arithmetic runs on the CPU in fp32 with bf16 rounding.
+
+    Returns dict(out [n, H] bf16, grad_hidden [n, H] bf16,
+    grad_routing_weights [n, k] fp32) in the order of ``tokens``.
+    """
+    kw = _act_kw(act_kw)
+    tokens = [int(t) for t in tokens]
+    E, H, two_i = gate_up.shape
+    sel = selected.cpu().long()
+    k = sel.shape[1]
+    by_expert: dict = {}
+    for n, t in enumerate(tokens):
+        for j in range(k):
+            e = int(sel[t, j])
+            if 0 <= e < E:
+                by_expert.setdefault(e, []).append((n, j))
+    xs = x[tokens].float().cpu()
+    dys = dy[tokens].float().cpu()
+    ws = rw[tokens].float().cpu()
+    y_rows, dx_rows = {}, {}
+    grad_rw = torch.zeros(len(tokens), k)
+    for e in sorted(by_expert):
+        nj = by_expert[e]
+        idx = torch.tensor([n for n, _ in nj])
+        slot = torch.tensor([j for _, j in nj])
+        r = _expert_rows(xs[idx], dys[idx], ws[idx, slot], gate_up[e].cpu().float(), down[e].cpu().float(), *kw)
+        for i, (n, j) in enumerate(nj):
+            y_rows[n, j] = r["y"][i]
+            dx_rows[n, j] = r["dx"][i]
+            grad_rw[n, j] = r["dscale"][i]
+    out = torch.zeros(len(tokens), H)
+    grad_hidden = torch.zeros(len(tokens), H)
+    for n in range(len(tokens)):
+        for j in range(k):                     # fp32 sum in slot order
+            if (n, j) in y_rows:
+                out[n] += y_rows[n, j]
+                grad_hidden[n] += dx_rows[n, j]
+    return dict(out=out.to(torch.bfloat16), grad_hidden=grad_hidden.to(torch.bfloat16), grad_routing_weights=grad_rw)
+
+
+def backward_expert(x, selected, gate_up, down, rw, dy, expert, **act_kw):
+    """Weight gradients of one expert (backward steps 3 and 5 of
+    tests/_moe_baselines.py:96-226): grad_fc2[e] = bf16(gco_e^T act_e) [H, I]
+    and grad_gate_up[e] = bf16(x_e^T dAB_e) [H, 2I], over the expert's rows in
+    the stable expert-major order (ascending flat route id). Inputs may live
+    on any device; returns (grad_gate_up_e, grad_fc2_e) bf16 on the CPU.
+    """
+    kw = _act_kw(act_kw)
+    E, H, two_i = gate_up.shape
+    e = int(expert)
+    flat = selected.cpu().long().reshape(-1)
+    routes = torch.nonzero(flat == e).reshape(-1)            # ascending = stable order
+    k = selected.shape[1]
+    if routes.numel() == 0:
+        z = torch.zeros
+        return z(H, two_i, dtype=torch.bfloat16), z(H, two_i // 2, dtype=torch.bfloat16)
+    toks = routes // k
+    dev_toks = toks.to(x.device)
+    xr = x.index_select(0, dev_toks).float().cpu()
+    dyr = dy.index_select(0, dev_toks).float().cpu()
+    wr = rw.reshape(-1).index_select(0, routes.to(rw.device)).float().cpu()
+    r = _expert_rows(xr, dyr, wr, gate_up[e].cpu().float(), down[e].cpu().float(), *kw)
+    return bf16(xr.T @ r["dab"]).to(torch.bfloat16), bf16(r["gco"].T @ r["act"]).to(torch.bfloat16)
 
 
 # --------------------------------------------------------------------- fp64 autograd restatement

@@ -50,6 +50,16 @@ def test_constructor_rejects_nonpositive(kw):
         mega_moe.FusedMoEForward(None, **base)
 
 
+@pytest.mark.parametrize("kw", [dict(top_k=65)])
+def test_constructor_rejects_kernel_limits(kw):
+    """Limits of the device kernels are rejected up front, not at the first
+    forward (combine slots: top_k <= 64)."""
+    base = dict(max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4)
+    base.update(kw)
+    with pytest.raises(ValueError):
+        mega_moe.FusedMoEForward(None, **base)
+
+
 def test_constructor_type_and_unbuilt_features():
     with pytest.raises(TypeError):
         mega_moe.FusedMoEForward(None, max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4, config={})

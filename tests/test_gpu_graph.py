@@ -68,3 +68,47 @@ def test_captured_step_replays_bit_exact(spec):
         torch.cuda.synchronize()
         for name, got, exp in zip(("output",) + GRADS, again, want):
             assert torch.equal(got, exp), f"eager after replay {rep}: {name} differs"
+
+
+def test_graphs_of_two_sizes_on_one_stream():
+    """Graphs captured for a small and then a large batch on one stream, the
+    small one replayed after the large one: the operator's workspaces are
+    sized for max_tokens_per_rank before the first capture, so neither graph
+    holds a freed workspace address; a direct wrapper call that outgrows the
+    module pool retires its old buffer instead of freeing it."""
+    from mega_moe.ops import _kernels as K
+
+    spec = CaseSpec("graph_sizes", 512, 256, 256, 8, 4, "softmax_topk", True)
+    inp = make_inputs(spec, device="cuda", seed=8, weight_scale=0.1)
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=spec.tokens, hidden_size=spec.hidden,
+                                  top_k=spec.top_k, num_experts=spec.experts)
+    sizes = (64, 512)
+    parts = {n: {k: (v[:n].clone() if k in ("x", "dy", "selected", "rw") else v) for k, v in inp.items()}
+             for n in sizes}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = {n: [t.clone() for t in _step(op, parts[n])] for n in sizes}
+    torch.cuda.synchronize()
+    before = op._workspaces.nbytes()
+    graphs, outs = {}, {}
+    for n in sizes:                                   # small first, then large
+        graphs[n] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[n], stream=side):
+            outs[n] = _step(op, parts[n])
+    torch.cuda.synchronize()
+    assert op._workspaces.nbytes() == before          # nothing grew under capture
+    junk = [torch.full((1 << 20,), 7, dtype=torch.int32, device="cuda") for _ in range(8)]
+    for n in (512, 64, 512, 64):
+        graphs[n].replay()
+        torch.cuda.synchronize()
+        for name, got, exp in zip(("output",) + GRADS, outs[n], eager[n]):
+            assert torch.equal(got, exp), f"tokens={n}: {name} differs from the eager result"
+    del junk
+    # module pool: growth retires, never frees
+    pool = K.WorkspacePool()
+    a = pool.get(torch.device("cuda"), 1024, "t")
+    b = pool.get(torch.device("cuda"), 4096, "t")
+    assert a.data_ptr() != b.data_ptr() and pool.nbytes() == a.numel() + b.numel()
+    pool.release()
+    assert pool.nbytes() == 0

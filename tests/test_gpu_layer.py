@@ -107,24 +107,72 @@ def test_autograd_function_matches_backward(fmt):
     del out3
 
 
+def _sample_tokens(ref, spec, experts, n):
+    """Tokens whose rows sit where tiling goes wrong first: the first and last
+    rows of the given experts (hottest: longest run of full tiles; ragged:
+    a short last tile), the first and last token, then evenly spaced tokens
+    up to ``n``."""
+    off, st = ref["offsets"], ref["send_token"]
+    picks = [0, spec.tokens - 1]
+    for e in experts:
+        a, b = int(off[e]), int(off[e + 1])
+        picks += [int(t) for t in st[a:min(b, a + 4)]] + [int(t) for t in st[max(a, b - 8):b]]
+    step = max(1, spec.tokens // n)
+    t = 1
+    while len(dict.fromkeys(picks)) < n:
+        picks.append(t)
+        t = (t + step) % spec.tokens
+    return list(dict.fromkeys(picks))[:n]
+
+
+def _probe_experts(counts):
+    """(hottest, median, ragged): the ragged one has the shortest non-empty
+    remainder past a multiple of 128 rows (a last tile holding a few rows)."""
+    order = sorted(range(len(counts)), key=lambda e: (int(counts[e]), e))
+    hottest, median = order[-1], order[len(order) // 2]
+    rag = [e for e in order if counts[e] % 128 and e not in (hottest, median)]
+    ragged = min(rag, key=lambda e: (int(counts[e]) % 128, -int(counts[e]))) if rag else order[0]
+    return hottest, median, ragged
+
+
 @pytest.mark.parametrize("name", ["e32", "qwen", "skew", "kimi"])
 def test_full_size_sampled_parity(name):
-    """BASELINE sizes: routing bit-exact and sampled output rows vs the oracle."""
+    """BASELINE sizes and seeds, forward + backward: routing bit-exact; output
+    rows, grad_hidden rows and grad_routing_weights rows of 64 sampled
+    tokens (hottest expert, a ragged last tile, spread tokens); the full
+    weight gradients of three experts (hottest, median, ragged) -- all
+    against the CPU oracle, max relative error <= 2e-2 plus the reference's
+    GRAD element check. (E32 is a forward-only config; its backward is
+    checked too.)"""
     spec = CASES[name]
     inp = make_inputs(spec, device="cuda", seed=1234)
     op = _op(spec)
-    out = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"])
-    tables = op._route(inp["selected"], inp["rw"])
+    x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
+    out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, dy)
     torch.cuda.synchronize()
-    ref = O.route(inp["selected"].cpu().numpy(), spec.experts, spec.top_k)
+    ref = O.route(sel.cpu().numpy(), spec.experts, spec.top_k)
     nv = int(ref["offsets"][-1])
-    assert tables.send_route[:nv].cpu().numpy().tolist() == ref["send_route"].tolist()
-    assert tables.route_to_send.cpu().numpy().tolist() == ref["route_to_send"].tolist()
-    toks = [0, 1, spec.tokens // 2, spec.tokens - 1]
-    sub = O.forward_tokens(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"], inp["down"], inp["rw"].cpu(),
-                           toks)
-    assert_rel(out[toks], sub, 2e-2, f"{name} sampled rows")
-    del inp, out
+    assert saved["split_size_cum_per_expert"].cpu().numpy().tolist() == ref["offsets"].tolist()
+    assert saved["send_route_indices"][:nv].cpu().numpy().tolist() == ref["send_route"].tolist()
+    assert saved["send_token_indices"][:nv].cpu().numpy().tolist() == ref["send_token"].tolist()
+    assert saved["route_to_send"].cpu().numpy().tolist() == ref["route_to_send"].tolist()
+    experts = _probe_experts(ref["counts"])
+    print(f"[{name}] probe experts (hottest, median, ragged) = {experts}, rows = "
+          f"{[int(ref['counts'][e]) for e in experts]}", flush=True)
+    toks = _sample_tokens(ref, spec, (experts[0], experts[2]), 64)
+    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks)
+    assert_rel(out[toks], sub["out"], 2e-2, f"{name} output rows")
+    for key in ("grad_hidden", "grad_routing_weights"):
+        assert_rel(g[key][toks], sub[key], 2e-2, f"{name} {key} rows")
+        assert cmp_grad(g[key][toks], sub[key], GRAD_RTOL, GRAD_ATOL) == 0, key
+    for e in experts:
+        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e)
+        assert_rel(g["grad_gate_up"][e], dgu, 2e-2, f"{name} grad_gate_up[{e}]")
+        assert_rel(g["grad_fc2"][e], dfc2, 2e-2, f"{name} grad_fc2[{e}]")
+        assert cmp_grad(g["grad_gate_up"][e], dgu, GRAD_RTOL, GRAD_ATOL) == 0
+        assert cmp_grad(g["grad_fc2"][e], dfc2, GRAD_RTOL, GRAD_ATOL) == 0
+    del inp, out, saved, g, x, sel, w1, w2, rw, dy
     torch.cuda.empty_cache()
 
 
@@ -161,6 +209,21 @@ def test_empty_batch():
     x0 = inp["x"][:0]
     out = op.forward(x0, inp["selected"][:0], inp["gate_up"], inp["down"], inp["rw"][:0])
     assert out.shape == (0, spec.hidden)
+    # backward of an empty batch: empty input gradients, zero weight gradients
+    out, saved = op.forward(x0, inp["selected"][:0], inp["gate_up"], inp["down"], inp["rw"][:0],
+                            return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, inp["dy"][:0])
+    assert g["grad_hidden"].shape == (0, spec.hidden) and g["grad_routing_weights"].shape == (0, spec.top_k)
+    assert g["grad_gate_up"].shape == inp["gate_up"].shape and torch.count_nonzero(g["grad_gate_up"]) == 0
+    assert g["grad_fc2"].shape == inp["down"].shape and torch.count_nonzero(g["grad_fc2"]) == 0
+    # and through the autograd function
+    x = x0.clone().requires_grad_(True)
+    rw = inp["rw"][:0].clone().requires_grad_(True)
+    w1 = inp["gate_up"].clone().requires_grad_(True)
+    w2 = inp["down"].contiguous().requires_grad_(True)
+    y = mega_moe.MegaMoEFunction.apply(op, x, rw, inp["selected"][:0], w1, w2, torch.empty(1, device="cuda"), None)
+    y.sum().backward()
+    assert x.grad.shape == x0.shape and torch.count_nonzero(w1.grad) == 0 and torch.count_nonzero(w2.grad) == 0
 
 
 def test_all_routes_dropped_and_one_hot_expert():

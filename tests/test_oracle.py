@@ -251,3 +251,45 @@ def test_backward_recompute_act_matches_saved_for_bf16():
     a, b = O.backward(st, dy), O.backward(st, dy, recompute_act=True)
     for key in ("grad_hidden", "grad_fc2", "grad_gate_up", "grad_routing_weights"):
         assert torch.equal(a[key], b[key])
+
+
+# --------------------------------------------------------------------- sampled backward helpers
+@pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu", "situglu"])
+def test_backward_tokens_equals_full_backward(activation):
+    """backward_tokens over every token evaluates each expert's complete row
+    set with the same GEMM shapes as forward/backward: bit-identical output,
+    grad_hidden and grad_routing_weights. A subset agrees to bf16 rounding
+    (the only difference is the GEMM's row count)."""
+    x, sel, w1, w2, rw, dy = _small_case(seed=5, T=40, E=6, k=3)
+    kw = dict(activation=activation, situ_beta=1.5, situ_linear_beta=2.0 if activation == "situglu" else None,
+              clamp_limit=0.3)
+    out, st = O.forward(x, sel, w1, w2, rw, **kw)
+    g = O.backward(st, dy)
+    full = O.backward_tokens(x, sel, w1, w2, rw, dy, range(x.shape[0]), **kw)
+    assert torch.equal(full["out"], out)
+    assert torch.equal(full["grad_hidden"], g["grad_hidden"])
+    assert torch.equal(full["grad_routing_weights"], g["grad_routing_weights"])
+    toks = [0, 3, 17, 39]
+    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks, **kw)
+    for name, ref in (("out", out), ("grad_hidden", g["grad_hidden"])):
+        d = (sub[name].float() - ref[toks].float()).abs()
+        assert float(d.max()) <= 2 ** -7 * float(ref[toks].float().abs().max()), name
+    d = (sub["grad_routing_weights"] - g["grad_routing_weights"][toks]).abs()
+    assert float(d.max()) <= 2 ** -7 * float(g["grad_routing_weights"].abs().max())
+    assert sub["grad_routing_weights"][0, 0] == 0          # dropped route
+
+
+@pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu"])
+def test_backward_expert_equals_full_backward(activation):
+    """backward_expert(e) is the e-th slice of the full weight gradients, bit
+    for bit, for every expert (including one with no rows)."""
+    x, sel, w1, w2, rw, dy = _small_case(seed=6, T=30, E=7, k=2)
+    sel[sel == 4] = 6                                        # expert 4 gets no rows
+    kw = dict(activation=activation, clamp_limit=0.3)
+    _, st = O.forward(x, sel, w1, w2, rw, **kw)
+    g = O.backward(st, dy)
+    for e in range(7):
+        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e, **kw)
+        assert torch.equal(dgu, g["grad_gate_up"][e]), e
+        assert torch.equal(dfc2, g["grad_fc2"][e]), e
+    assert torch.count_nonzero(g["grad_gate_up"][4]) == 0
