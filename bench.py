@@ -81,9 +81,9 @@ STAGE_KERNELS = {
 
 # CPU-baseline sample per config: (tokens, experts). Where the layer's experts
 # are spread evenly, the sample is an expert shard with the same rows per
-# expert (Kimi: 1/32 of the experts and of the tokens, 73 rows per expert as
+# expert (Kimi: 1/16 of the experts and of the tokens, 73 rows per expert as
 # in the full layer); Skew keeps all 32 experts so the Zipf skew is preserved.
-CPU_SAMPLE = {"toy": (512, 8), "e32": (1024, 8), "qwen": (1024, 16), "kimi": (128, 28), "skew": (2048, 32)}
+CPU_SAMPLE = {"toy": (512, 8), "e32": (1024, 8), "qwen": (1024, 16), "kimi": (256, 56), "skew": (2048, 32)}
 
 
 def cpu_inputs(spec, tokens: int, experts: int, seed: int = 99):
