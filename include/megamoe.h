@@ -86,6 +86,26 @@ int mm_route(const int32_t* selected, int64_t num_routes, int32_t top_k,
              int32_t* send_token, int32_t* route_to_send, float* weight_perm,
              void* workspace, size_t workspace_bytes, mm_stream_t stream);
 
+/*
+ * mm_route without a workspace argument: the per-unit count table lives in
+ * a library-owned device array of mm_route_noalloc_scratch_bytes() bytes
+ * (4 MiB) per GPU, kept until the process ends. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, outputs and errors as mm_route; calls whose
+ * mm_route_workspace_bytes(num_routes, num_experts) exceeds the scratch size
+ * return MM_E_ARG (with E = 1024 that allows about 2 million routes). The
+ * call allocates nothing. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams) race.
+ */
+size_t mm_route_noalloc_scratch_bytes(void);
+
+int mm_route_noalloc(const int32_t* selected, int64_t num_routes, int32_t top_k,
+                     int32_t num_experts, const float* routing_weights,
+                     int32_t* counts, int32_t* offsets, int32_t* send_route,
+                     int32_t* send_token, int32_t* route_to_send,
+                     float* weight_perm, mm_stream_t stream);
+
 /* ---------------------------------------------------------------- permute */
 
 /*

@@ -17,6 +17,8 @@
 //                    from ballot "match" masks, across the four wavefronts from
 //                    tagged LDS counters, so the scatter is stable without a
 //                    sort and writes every table exactly once.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -171,28 +173,14 @@ extern "C" size_t mm_route_workspace_bytes(int64_t num_routes, int32_t num_exper
   return mm_align_up(static_cast<size_t>(nunits) * static_cast<size_t>(num_experts) * 4 + 256, 256);
 }
 
-extern "C" int mm_route(const int32_t* selected, int64_t num_routes, int32_t top_k, int32_t num_experts,
-                        const float* routing_weights, int32_t* counts, int32_t* offsets,
-                        int32_t* send_route, int32_t* send_token, int32_t* route_to_send,
-                        float* weight_perm, void* workspace, size_t workspace_bytes,
-                        mm_stream_t stream) {
-  MM_CHECK_ARG(num_routes >= 0 && num_routes < (int64_t(1) << 31), "mm_route: num_routes out of range");
-  MM_CHECK_ARG(top_k > 0, "mm_route: top_k must be positive");
-  MM_CHECK_ARG(num_experts > 0 && num_experts <= kMaxExperts, "mm_route: num_experts must be in [1, %d]",
-               kMaxExperts);
-  MM_CHECK_ARG(counts && offsets, "mm_route: counts/offsets must be non-null");
-  MM_CHECK_ARG(num_routes == 0 || (selected && send_route && send_token && route_to_send),
-               "mm_route: route tables must be non-null");
-  MM_CHECK_ARG((weight_perm == nullptr) == (routing_weights == nullptr),
-               "mm_route: routing_weights and weight_perm must be given together");
-  if (workspace_bytes < mm_route_workspace_bytes(num_routes, num_experts) || workspace == nullptr) {
-    mm_set_error("mm_route: workspace too small");
-    return MM_E_WS;
-  }
-  hipStream_t s = mm_hip_stream(stream);
+namespace {
+
+int route_launch(const int32_t* selected, int64_t num_routes, int32_t top_k, int32_t num_experts,
+                 const float* routing_weights, int32_t* counts, int32_t* offsets, int32_t* send_route,
+                 int32_t* send_token, int32_t* route_to_send, float* weight_perm, int32_t* unit_counts,
+                 hipStream_t s, const char* what) {
   const int E = num_experts;
   const int nunits = static_cast<int>((num_routes + kChunk - 1) / kChunk);
-  int32_t* unit_counts = static_cast<int32_t*>(workspace);
   if (nunits > 0) {
     route_count_kernel<<<nunits, kThreads, E * sizeof(int), s>>>(selected, num_routes, E, nunits,
                                                                  unit_counts);
@@ -205,5 +193,94 @@ extern "C" int mm_route(const int32_t* selected, int64_t num_routes, int32_t top
                                                        routing_weights, send_route, send_token,
                                                        route_to_send, weight_perm);
   }
-  return mm_check_launch("mm_route");
+  return mm_check_launch(what);
+}
+
+}  // namespace
+
+#define MM_ROUTE_CHECK_ARGS(what)                                                                          \
+  MM_CHECK_ARG(num_routes >= 0 && num_routes < (int64_t(1) << 31), what ": num_routes out of range");     \
+  MM_CHECK_ARG(top_k > 0, what ": top_k must be positive");                                                \
+  MM_CHECK_ARG(num_experts > 0 && num_experts <= kMaxExperts, what ": num_experts must be in [1, %d]",     \
+               kMaxExperts);                                                                               \
+  MM_CHECK_ARG(counts && offsets, what ": counts/offsets must be non-null");                               \
+  MM_CHECK_ARG(num_routes == 0 || (selected && send_route && send_token && route_to_send),                 \
+               what ": route tables must be non-null");                                                    \
+  MM_CHECK_ARG((weight_perm == nullptr) == (routing_weights == nullptr),                                   \
+               what ": routing_weights and weight_perm must be given together")
+
+extern "C" int mm_route(const int32_t* selected, int64_t num_routes, int32_t top_k, int32_t num_experts,
+                        const float* routing_weights, int32_t* counts, int32_t* offsets,
+                        int32_t* send_route, int32_t* send_token, int32_t* route_to_send,
+                        float* weight_perm, void* workspace, size_t workspace_bytes,
+                        mm_stream_t stream) {
+  MM_ROUTE_CHECK_ARGS("mm_route");
+  if (workspace_bytes < mm_route_workspace_bytes(num_routes, num_experts) || workspace == nullptr) {
+    mm_set_error("mm_route: workspace too small");
+    return MM_E_WS;
+  }
+  return route_launch(selected, num_routes, top_k, num_experts, routing_weights, counts, offsets, send_route,
+                      send_token, route_to_send, weight_perm, static_cast<int32_t*>(workspace),
+                      mm_hip_stream(stream), "mm_route");
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+//
+// mm_route_noalloc keeps the per-unit count table (the only scratch mm_route
+// uses) in a file-scope device array instead of a caller workspace. Every
+// GPU the library runs on holds its own copy until the process ends; the
+// host reaches it through the address hipGetSymbolAddress returns on that
+// device (the array's name in host code is only a stand-in). The table is
+// fully rewritten by route_count_kernel on every call, so nothing needs
+// clearing; calls that overlap on one GPU (different streams) race on it.
+namespace {
+
+constexpr size_t kRouteScratchBytes = size_t(4) << 20;  // 4 MiB
+static __device__ __align__(256) int32_t scratch[kRouteScratchBytes / sizeof(int32_t)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int scratch_for_current_device(int32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    mm_set_error("mm_route_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return MM_E_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      mm_set_error("mm_route_noalloc: hipGetSymbolAddress failed (%s)", hipGetErrorString(e));
+      return MM_E_LAUNCH;
+    }
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return MM_OK;
+}
+
+}  // namespace
+
+extern "C" size_t mm_route_noalloc_scratch_bytes(void) { return kRouteScratchBytes; }
+
+extern "C" int mm_route_noalloc(const int32_t* selected, int64_t num_routes, int32_t top_k,
+                                int32_t num_experts, const float* routing_weights, int32_t* counts,
+                                int32_t* offsets, int32_t* send_route, int32_t* send_token,
+                                int32_t* route_to_send, float* weight_perm, mm_stream_t stream) {
+  MM_ROUTE_CHECK_ARGS("mm_route_noalloc");
+  const size_t need = mm_route_workspace_bytes(num_routes, num_experts);
+  if (need > kRouteScratchBytes) {
+    mm_set_error("mm_route_noalloc: %lld routes x %d experts need %zu bytes of scratch, above the %zu-byte "
+                 "maximum; use mm_route with a workspace",
+                 static_cast<long long>(num_routes), num_experts, need, kRouteScratchBytes);
+    return MM_E_ARG;
+  }
+  int32_t* ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws)) return rc;
+  return route_launch(selected, num_routes, top_k, num_experts, routing_weights, counts, offsets, send_route,
+                      send_token, route_to_send, weight_perm, ws, mm_hip_stream(stream), "mm_route_noalloc");
 }

@@ -33,6 +33,8 @@ SIGNATURES = {
     "mm_version": (ctypes.c_int, []),
     "mm_route_workspace_bytes": (_SZ, [_I64, _I32]),
     "mm_route": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "mm_route_noalloc_scratch_bytes": (_SZ, []),
+    "mm_route_noalloc": (ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "mm_permute": (ctypes.c_int, [_P, _I64, _P, _P, _I32, _I64, _I32, _P, _I64, _P]),
     "mm_gemm_workspace_bytes": (_SZ, [_I64, _I32]),
     "mm_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
