@@ -73,61 +73,62 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const uint4* __restri
 }
 
 // out[t] = bf16(sum_j fp32(y[route_to_send[t*k+j]])), slot order j = 0..k-1.
-// c_split wavefronts share a token row (interleaved passes of 64 * VPL
-// vectors); each lane handles VPL 16-byte vectors per pass and issues the
-// loads of SLOTS slots for all of them before accumulating, so SLOTS * VPL
-// row reads are in flight per lane (one round trip per pass for top-8).
-// Rows are read once: non-temporal loads.
+// Work is split into equal items: item i = (token i / nchunks, chunk
+// i % nchunks of 64 * VPL vectors), one wavefront per item, so every item
+// moves the same bytes (against up to 4 wavefronts per token interleaving
+// 2 KiB passes, whose last pass per token was short: Kimi shape 181 -> 176
+// us, Skew 213 -> 204 us). Each lane issues the loads of SLOTS slots for its
+// VPL vectors before accumulating (SLOTS * VPL row reads in flight per lane;
+// one round trip per 8 slots). Rows are read once: non-temporal loads.
 template <int VPL, int SLOTS>
-__global__ __launch_bounds__(kThreads) void combine_kernel(const uint4* __restrict__ y, int64_t ldy_v,
-                                                           const int32_t* __restrict__ route_to_send,
-                                                           int64_t T, int top_k, int hidden_v,
-                                                           uint4* __restrict__ out, int64_t ldo_v, int c_split) {
+__global__ __launch_bounds__(kThreads) void combine_items_kernel(const uint4* __restrict__ y, int64_t ldy_v,
+                                                                 const int32_t* __restrict__ route_to_send,
+                                                                 int64_t T, int top_k, int hidden_v,
+                                                                 uint4* __restrict__ out, int64_t ldo_v,
+                                                                 int nchunks) {
   const int lane = threadIdx.x & 63;
-  const int split = c_split;
-  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6); w < T * split;
+  const int64_t items = T * nchunks;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6); w < items;
        w += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
-    const int64_t t = w / split;
-    const int part = static_cast<int>(w % split);
+    const int64_t t = w / nchunks;
+    const int v0 = static_cast<int>(w % nchunks) * 64 * VPL + lane;
     const int my_row = lane < top_k ? route_to_send[t * top_k + lane] : -1;
-    uint4* dst = out + t * ldo_v;
-    for (int v0 = lane + part * 64 * VPL; v0 < hidden_v; v0 += 64 * VPL * split) {
-      float acc[VPL][8];
+    float acc[VPL][8];
 #pragma unroll
-      for (int u = 0; u < VPL; ++u)
+    for (int u = 0; u < VPL; ++u)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[u][q] = 0.0f;
-      for (int j0 = 0; j0 < top_k; j0 += SLOTS) {
-        uint4 val[SLOTS][VPL];
-        int rr[SLOTS];
+      for (int q = 0; q < 8; ++q) acc[u][q] = 0.0f;
+    for (int j0 = 0; j0 < top_k; j0 += SLOTS) {
+      uint4 val[SLOTS][VPL];
+      int rr[SLOTS];
 #pragma unroll
-        for (int jj = 0; jj < SLOTS; ++jj) {
-          const int j = j0 + jj;
-          rr[jj] = __shfl(my_row, j < top_k ? j : 0);
-          if (j >= top_k) rr[jj] = -1;
+      for (int jj = 0; jj < SLOTS; ++jj) {
+        const int j = j0 + jj;
+        rr[jj] = __shfl(my_row, j < top_k ? j : 0);
+        if (j >= top_k) rr[jj] = -1;
 #pragma unroll
-          for (int u = 0; u < VPL; ++u) {
-            const int v = v0 + u * 64;
-            val[jj][u] = (rr[jj] >= 0 && v < hidden_v) ? load_stream16(y + static_cast<int64_t>(rr[jj]) * ldy_v + v)
-                                                        : make_uint4(0, 0, 0, 0);
-          }
-        }
-#pragma unroll
-        for (int jj = 0; jj < SLOTS; ++jj) {
-          if (rr[jj] < 0) continue;
-#pragma unroll
-          for (int u = 0; u < VPL; ++u) {
-            float f[8];
-            vec8_to_f32(val[jj][u], f);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc[u][q] += f[q];
-          }
+        for (int u = 0; u < VPL; ++u) {
+          const int v = v0 + u * 64;
+          val[jj][u] = (rr[jj] >= 0 && v < hidden_v) ? load_stream16(y + static_cast<int64_t>(rr[jj]) * ldy_v + v)
+                                                      : make_uint4(0, 0, 0, 0);
         }
       }
 #pragma unroll
-      for (int u = 0; u < VPL; ++u)
-        if (v0 + u * 64 < hidden_v) dst[v0 + u * 64] = f32_to_vec8(acc[u]);
+      for (int jj = 0; jj < SLOTS; ++jj) {
+        if (rr[jj] < 0) continue;
+#pragma unroll
+        for (int u = 0; u < VPL; ++u) {
+          float f[8];
+          vec8_to_f32(val[jj][u], f);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[u][q] += f[q];
+        }
+      }
     }
+    uint4* dst = out + t * ldo_v;
+#pragma unroll
+    for (int u = 0; u < VPL; ++u)
+      if (v0 + u * 64 < hidden_v) dst[v0 + u * 64] = f32_to_vec8(acc[u]);
   }
 }
 
@@ -344,15 +345,12 @@ extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_t
   MM_CHECK_ARG(y && route_to_send && out, "mm_combine: null pointer");
   MM_CHECK_ARG(hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) && aligned16(out),
                "mm_combine: rows must be 16-byte aligned");
-  // up to 4 wavefronts per token row (interleaved 2 KiB passes) so that small
-  // batches of long rows still keep >= 16K rows' worth of loads in flight
-  // (Kimi shape: 4.9 -> 5.6 TB/s)
-  const int64_t passes = (hidden / 8 + 127) / 128;
-  const int split = static_cast<int>(std::min<int64_t>(std::min<int64_t>(passes, 4),
-                                                        std::max<int64_t>(1, (16384 + num_tokens - 1) / num_tokens)));
-  combine_kernel<2, 8><<<grid_for_rows(num_tokens * split), kThreads, 0, mm_hip_stream(stream)>>>(
+  const int nchunks = (hidden / 8 + 127) / 128;
+  int64_t g = (num_tokens * nchunks + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (g > 65536) g = 65536;
+  combine_items_kernel<2, 8><<<static_cast<int>(g), kThreads, 0, mm_hip_stream(stream)>>>(
       reinterpret_cast<const uint4*>(y), ldy / 8, route_to_send, num_tokens, top_k, hidden / 8,
-      reinterpret_cast<uint4*>(out), ldo / 8, split);
+      reinterpret_cast<uint4*>(out), ldo / 8, nchunks);
   return mm_check_launch("mm_combine");
 }
 

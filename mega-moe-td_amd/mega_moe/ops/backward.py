@@ -16,7 +16,8 @@ hand-written reference backward it is checked against
 
 Returned keys follow the reference: grad_hidden, grad_routing_weights,
 grad_fc1_1 / grad_fc1_2 ([E, F, H] views), grad_fc2 ([E, H, F]) and the
-intermediates grad_swiglu, grad_fc1_output, grad_gate, grad_fc1; plus
+intermediates grad_swiglu, grad_fc1_output, grad_gate, grad_fc1 (plus
+grad_fc2_out_sorted and grad_recv_hidden_sorted, derived when read); plus
 grad_gate_up, the packed [E, H, 2F] weight gradient.
 """
 
@@ -103,12 +104,55 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     grad_gate_up = K.grouped_wgrad(x, send_token, dab, None, offsets, H, 2 * inter, pool=pool, ws_rows=ws_rows)
     tm.end()
 
-    return _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter)
+    grads = _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter)
+    grads._bind(dy, send_token, offsets, dx)
+    return grads
+
+
+class MoEGrads(dict):
+    """Gradient dict of ``moe_backward_triton``.
+
+    Besides the gradients it derives, on first read, the two expert-major
+    intermediates the reference exposes for per-stage checks
+    (tests/_moe_baselines.py:208-225, ops/backward.py:384-399):
+    ``grad_fc2_out_sorted`` = dy gathered to the expert-major rows [M, H]
+    (the backward's GEMMs read it in place, so it is materialised only when
+    asked for) and ``grad_recv_hidden_sorted`` = the FC1 input gradient
+    [M, H] before the top-k reduce. M = number of valid routes (one host
+    read of the routing offsets).
+    """
+
+    _DERIVED = ("grad_fc2_out_sorted", "grad_recv_hidden_sorted")
+
+    def _bind(self, dy, send_token, offsets, dx):
+        self._src = (dy, send_token, offsets, dx)
+
+    def __missing__(self, key):
+        src = getattr(self, "_src", None)
+        if key not in self._DERIVED or src is None:
+            raise KeyError(key)
+        dy, send_token, offsets, dx = src
+        m = int(offsets[-1].item())
+        if key == "grad_fc2_out_sorted":
+            value = K.permute(dy, send_token, offsets, m) if m else dy[:0].clone()
+        else:
+            value = dx[:m]
+        self[key] = value
+        return value
+
+    def __contains__(self, key):
+        return dict.__contains__(self, key) or (key in self._DERIVED and getattr(self, "_src", None) is not None)
+
+    def get(self, key, default=None):
+        try:
+            return self[key]
+        except KeyError:
+            return default
 
 
 def _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter):
     grad_fc1 = grad_gate_up.transpose(1, 2)  # [E, 2F, H] view
-    return dict(
+    return MoEGrads(
         grad_hidden=grad_hidden,
         grad_routing_weights=grad_rw,
         grad_fc1_1=grad_fc1[:, :inter],
@@ -131,10 +175,13 @@ def _empty_batch_grads(saved, dy):
     w1 = saved["gate_up_weight"]
     dev, bf = w1.device, torch.bfloat16
     E = w1.shape[0]
-    return _grad_dict(torch.empty(0, H, dtype=bf, device=dev), torch.empty(0, k, dtype=torch.float32, device=dev),
-                      torch.zeros(E, H, inter, dtype=bf, device=dev), torch.zeros(E, H, 2 * inter, dtype=bf, device=dev),
-                      torch.empty(0, inter, dtype=bf, device=dev), torch.empty(0, 2 * inter, dtype=bf, device=dev),
-                      torch.empty(0, dtype=bf, device=dev), inter)
+    grads = _grad_dict(torch.empty(0, H, dtype=bf, device=dev), torch.empty(0, k, dtype=torch.float32, device=dev),
+                       torch.zeros(E, H, inter, dtype=bf, device=dev), torch.zeros(E, H, 2 * inter, dtype=bf, device=dev),
+                       torch.empty(0, inter, dtype=bf, device=dev), torch.empty(0, 2 * inter, dtype=bf, device=dev),
+                       torch.empty(0, dtype=bf, device=dev), inter)
+    grads.update(grad_fc2_out_sorted=torch.empty(0, H, dtype=bf, device=dev),
+                 grad_recv_hidden_sorted=torch.empty(0, H, dtype=bf, device=dev))
+    return grads
 
 
 class MegaMoEBackwardFunction(torch.autograd.Function):
@@ -168,4 +215,4 @@ class MegaMoEBackwardFunction(torch.autograd.Function):
                 grads["grad_fc1_2"], grads["grad_fc2"], None, None, None)
 
 
-__all__ = ["MegaMoEBackwardFunction", "moe_backward_triton"]
+__all__ = ["MegaMoEBackwardFunction", "MoEGrads", "moe_backward_triton"]

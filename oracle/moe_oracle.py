@@ -313,6 +313,8 @@ def backward(state, dy, recompute_act=False):
         grad_swiglu=grad_act,
         grad_fc1_output=dab,
         grad_gate=dscale,
+        grad_fc2_out_sorted=gco,
+        grad_recv_hidden_sorted=dx,
     )
 
 

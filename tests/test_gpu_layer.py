@@ -52,6 +52,13 @@ def test_forward_backward_parity(spec, activation):
         assert_rel(g[name], ref[name], 2e-2, name)
         assert cmp_grad(g[name], ref[name], GRAD_RTOL, GRAD_ATOL) == 0, name
     assert g["grad_routing_weights"][0, 0] == 0 and g["grad_routing_weights"][5, 1] == 0
+    # expert-major intermediates (reference tests/_moe_baselines.py:208-225)
+    m = int(saved["split_size_cum_per_expert"][-1])
+    assert "grad_fc2_out_sorted" in g and g["grad_fc2_out_sorted"].shape == (m, spec.hidden)
+    assert torch.equal(g["grad_fc2_out_sorted"].float().cpu(), ref["grad_fc2_out_sorted"])
+    assert_rel(g["grad_recv_hidden_sorted"], ref["grad_recv_hidden_sorted"], 2e-2, "grad_recv_hidden_sorted")
+    assert_rel(g["grad_swiglu"][:m], ref["grad_swiglu"], 2e-2, "grad_swiglu")
+    assert_rel(g["grad_fc1_output"][:m], ref["grad_fc1_output"], 2e-2, "grad_fc1_output")
     # unpacked views follow the reference's [E, F, H] layout
     I = spec.inter
     assert torch.equal(g["grad_fc1_1"], g["grad_gate_up"][:, :, :I].transpose(1, 2))
