@@ -70,7 +70,9 @@ size_t mm_route_workspace_bytes(int64_t num_routes, int32_t num_experts);
  * (kernels/fc2_combine.py:508-529).
  *
  *   selected      [num_routes] int32 expert id per flat route (token*k + slot);
- *                 ids outside [0, num_experts) are dropped.
+ *                 ids outside [0, num_experts) are dropped. 1 <= num_experts
+ *                 <= 32768 (the large-bin-count range of runtime/routing.py:
+ *                 246-416).
  *   routing_weights [num_routes] fp32 or NULL.
  *   counts        [E]     routes per expert.
  *   offsets       [E+1]   exclusive prefix of counts; offsets[E] = #valid.

@@ -8,6 +8,10 @@
 // kernels/fc2_combine.py:508-529 inverts it (route_to_send, -1 for drops).
 //
 // MI355X design: three small launches, no global atomics, no host sync.
+// Up to 1024 experts the scatter runs four wavefronts per unit; above that
+// (up to 32768, bounded by LDS) one wavefront per unit, whose ballot match
+// masks alone give the stable rank (the reference's lower-bound path for
+// large bin counts, runtime/routing.py:246-416, serves the same range).
 //   1. route_count   one workgroup per chunk of ROUTE_CHUNK consecutive routes
 //                    builds an LDS histogram -> unit_counts[unit][expert].
 //   2. route_scan    one workgroup turns unit_counts into absolute start rows
@@ -27,7 +31,8 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kIters = 8;                       // 256-route steps per unit
 constexpr int kChunk = kThreads * kIters;       // routes per unit
-constexpr int kMaxExperts = 1024;               // LDS bound of route_scatter (36 KiB)
+constexpr int kMaxExperts4 = 1024;              // LDS bound of the 4-wave route_scatter (36 KiB)
+constexpr int kMaxExperts = 32768;              // LDS bound of the 1-wave scatter (128 KiB) and the scan
 
 __device__ __forceinline__ bool route_valid(int e, int E) { return e >= 0 && e < E; }
 
@@ -166,6 +171,52 @@ __global__ __launch_bounds__(kThreads) void route_scatter_kernel(
   }
 }
 
+// Scatter for large expert counts (E > kMaxExperts4): one wavefront per unit,
+// so the stable rank of a route among equal experts comes from the ballot
+// match mask alone and LDS holds only the E running row counters.
+__global__ __launch_bounds__(64) void route_scatter_wave_kernel(
+    const int32_t* __restrict__ sel, int64_t R, int top_k, int E, int nbits,
+    const int32_t* __restrict__ unit_base, const float* __restrict__ rw,
+    int32_t* __restrict__ send_route, int32_t* __restrict__ send_token,
+    int32_t* __restrict__ route_to_send, float* __restrict__ weight_perm) {
+  extern __shared__ int run[];  // [E] next free row of each expert
+  const int u = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = unit_base[static_cast<int64_t>(u) * E + e];
+  __syncthreads();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int64_t start = static_cast<int64_t>(u) * kChunk;
+  for (int it = 0; it < kChunk / 64; ++it) {
+    const int64_t i = start + static_cast<int64_t>(it) * 64 + lane;
+    const bool present = i < R;
+    const int e = present ? sel[i] : -1;
+    const bool valid = present && route_valid(e, E);
+    const int key = valid ? e : E;
+    uint64_t mask = __ballot(1);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      mask &= bit ? m : ~m;
+    }
+    const int rank = __popcll(mask & lt_mask);
+    const int base = valid ? run[key] : 0;
+    __syncthreads();  // every lane has read its expert's counter
+    if (present) {
+      if (valid) {
+        const int pos = base + rank;
+        send_route[pos] = static_cast<int32_t>(i);
+        send_token[pos] = static_cast<int32_t>(i / top_k);
+        route_to_send[i] = pos;
+        if (weight_perm != nullptr) weight_perm[pos] = rw[i];
+        if (rank == 0) run[key] = base + __popcll(mask);
+      } else {
+        route_to_send[i] = -1;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 extern "C" size_t mm_route_workspace_bytes(int64_t num_routes, int32_t num_experts) {
@@ -181,6 +232,19 @@ int route_launch(const int32_t* selected, int64_t num_routes, int32_t top_k, int
                  hipStream_t s, const char* what) {
   const int E = num_experts;
   const int nunits = static_cast<int>((num_routes + kChunk - 1) / kChunk);
+  if (E > kMaxExperts4) {
+    // dynamic LDS above 64 KiB (up to 132 KiB at kMaxExperts); set once
+    static std::once_flag once;
+    std::call_once(once, [] {
+      const int bytes = (kMaxExperts + 1024) * static_cast<int>(sizeof(int));
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(route_count_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(route_scan_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(route_scatter_wave_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    });
+  }
   if (nunits > 0) {
     route_count_kernel<<<nunits, kThreads, E * sizeof(int), s>>>(selected, num_routes, E, nunits,
                                                                  unit_counts);
@@ -188,10 +252,16 @@ int route_launch(const int32_t* selected, int64_t num_routes, int32_t top_k, int
   route_scan_kernel<<<1, 1024, (E + 1024) * sizeof(int), s>>>(unit_counts, E, nunits, counts, offsets);
   if (nunits > 0) {
     const int nbits = 32 - __builtin_clz(static_cast<unsigned>(E));
-    const size_t lds = static_cast<size_t>(E) * (1 + 2 * kWaves) * sizeof(int);
-    route_scatter_kernel<<<nunits, kThreads, lds, s>>>(selected, num_routes, top_k, E, nbits, unit_counts,
-                                                       routing_weights, send_route, send_token,
-                                                       route_to_send, weight_perm);
+    if (E <= kMaxExperts4) {
+      const size_t lds = static_cast<size_t>(E) * (1 + 2 * kWaves) * sizeof(int);
+      route_scatter_kernel<<<nunits, kThreads, lds, s>>>(selected, num_routes, top_k, E, nbits, unit_counts,
+                                                         routing_weights, send_route, send_token,
+                                                         route_to_send, weight_perm);
+    } else {
+      route_scatter_wave_kernel<<<nunits, 64, static_cast<size_t>(E) * sizeof(int), s>>>(
+          selected, num_routes, top_k, E, nbits, unit_counts, routing_weights, send_route, send_token,
+          route_to_send, weight_perm);
+    }
   }
   return mm_check_launch(what);
 }

@@ -35,7 +35,7 @@ from ..runtime.timing import NULL_TIMER
 from . import _kernels as K
 
 # Device-kernel limits (csrc/routing.hip kMaxExperts, csrc/rowops.hip combine slots).
-MAX_EXPERTS = 1024
+MAX_EXPERTS = 32768
 MAX_TOP_K = 64
 
 

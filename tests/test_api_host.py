@@ -50,10 +50,10 @@ def test_constructor_rejects_nonpositive(kw):
         mega_moe.FusedMoEForward(None, **base)
 
 
-@pytest.mark.parametrize("kw", [dict(top_k=65)])
+@pytest.mark.parametrize("kw", [dict(top_k=65), dict(num_experts=32769)])
 def test_constructor_rejects_kernel_limits(kw):
     """Limits of the device kernels are rejected up front, not at the first
-    forward (combine slots: top_k <= 64)."""
+    forward (combine slots: top_k <= 64; routing tables: E <= 32768)."""
     base = dict(max_tokens_per_rank=8, hidden_size=256, top_k=2, num_experts=4)
     base.update(kw)
     with pytest.raises(ValueError):

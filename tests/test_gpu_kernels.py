@@ -35,6 +35,11 @@ ROUTE_CASES = [
     (8192, 8, 128, "drops"),
     (16384, 8, 32, "zipf"),
     (2049, 5, 1024, "drops"),
+    # above 1024 experts: the one-wavefront scatter
+    (2049, 5, 1025, "drops"),
+    (4096, 8, 4096, "hot"),
+    (3000, 16, 20000, "drops"),
+    (700, 3, 32768, "uniform"),
 ]
 
 

@@ -233,6 +233,24 @@ def test_empty_batch():
     assert x.grad.shape == x0.shape and torch.count_nonzero(w1.grad) == 0 and torch.count_nonzero(w2.grad) == 0
 
 
+def test_many_experts_layer():
+    """E = 2048 (above the 4-wave scatter's 1024): forward + backward parity."""
+    spec = CaseSpec("many_experts", 512, 256, 128, 2048, 4, "softmax_topk", True)
+    inp = make_inputs(spec, device="cuda", seed=13, weight_scale=0.1)
+    op = _op(spec)
+    out, saved = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, inp["dy"])
+    torch.cuda.synchronize()
+    ref_out, st = O.forward(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"].cpu(), inp["down"].cpu(),
+                            inp["rw"].cpu())
+    ref = O.backward(st, inp["dy"].cpu())
+    nv = int(st["tables"]["offsets"][-1])
+    assert saved["send_route_indices"][:nv].cpu().numpy().tolist() == st["tables"]["send_route"].tolist()
+    assert_rel(out, ref_out, 2e-2, "out")
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up"):
+        assert_rel(g[name], ref[name], 2e-2, name)
+
+
 def test_all_routes_dropped_and_one_hot_expert():
     spec = SMALL[0]
     inp = make_inputs(spec, device="cuda", seed=4, weight_scale=0.1)
