@@ -1222,8 +1222,7 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
         a.ldq = n2;
         a.q_rows = nullptr;
       }
-      int g = device_cus() / kXcds * kXcds;
-      if (const char* ev = getenv("MM_WGRAD_GRID")) g = atoi(ev) / kXcds * kXcds;
+      const int g = device_cus() / kXcds * kXcds;
       wgrad_persist_kernel<kWideStages><<<g > 0 ? g : kXcds, 512, 0, s>>>(a, num_experts);
       return mm_check_launch("mm_grouped_wgrad");
     }
