@@ -319,7 +319,7 @@ def backward(state, dy, recompute_act=False):
 
 
 # --------------------------------------------------------------------- sampled backward
-def _expert_rows(xr, dyr, wr, w1e, w2e, activation, situ_beta, situ_linear_beta, clamp_limit):
+def _expert_rows(xr, dyr, wr, w1e, w2e, activation, situ_beta, situ_linear_beta, clamp_limit, save_fc1_dtype="bf16"):
     """Forward and backward quantities of one expert's rows (same rounding
     points as ``forward`` / ``backward``).
 
@@ -336,7 +336,11 @@ def _expert_rows(xr, dyr, wr, w1e, w2e, activation, situ_beta, situ_linear_beta,
     gco = bf16(dyr)
     grad_act = bf16(gco @ w2e)                                        # step 1
     scale = bf16(wr)[:, None]                                         # step 2
-    act_a, dact, v, dv = gated_act_grad(gate, up, activation, situ_beta, situ_linear_beta, clamp_limit)
+    # the backward reads the saved (maybe narrowed) FC1 output, as ``backward`` does
+    saved, sc = quantize_fc1(torch.cat([gate, up], dim=1), save_fc1_dtype)
+    gu = dequantize_fc1(saved, sc)
+    act_a, dact, v, dv = gated_act_grad(gu[:, :inter], gu[:, inter:], activation, situ_beta, situ_linear_beta,
+                                        clamp_limit)
     dab = bf16(torch.cat([grad_act * dact * v * scale, grad_act * act_a * dv * scale], dim=1))
     dscale = bf16((act_a * v * grad_act).sum(dim=1))
     dx = bf16(dab @ w1e.T)                                            # step 4a
@@ -345,7 +349,7 @@ def _expert_rows(xr, dyr, wr, w1e, w2e, activation, situ_beta, situ_linear_beta,
 
 def _act_kw(kw):
     return (kw.get("activation", "swiglu"), kw.get("situ_beta", 1.0), kw.get("situ_linear_beta"),
-            kw.get("clamp_limit", 7.0))
+            kw.get("clamp_limit", 7.0), kw.get("save_fc1_dtype", "bf16"))
 
 
 def backward_tokens(x, selected, gate_up, down, rw, dy, tokens, **act_kw):
@@ -357,7 +361,9 @@ def backward_tokens(x, selected, gate_up, down, rw, dy, tokens, **act_kw):
     grad_routing_weights = dscale of the route's row, 0 if dropped) for the
     routes of ``tokens``; the routes of one expert are evaluated together, so
     each expert's weights are read once. Inputs may live on any device; the
-    arithmetic runs on the CPU in fp32 with bf16 rounding.
+    arithmetic runs on the CPU in fp32 with bf16 rounding. ``act_kw`` takes
+    the activation arguments of ``forward`` and ``save_fc1_dtype`` (the
+    backward reads the saved FC1 output in that format, as ``backward`` does).
 
     Returns dict(out [n, H] bf16, grad_hidden [n, H] bf16,
     grad_routing_weights [n, k] fp32) in the order of ``tokens``.

@@ -142,18 +142,20 @@ def _probe_experts(counts):
     return hottest, median, ragged
 
 
-@pytest.mark.parametrize("name", ["e32", "qwen", "skew", "kimi"])
-def test_full_size_sampled_parity(name):
+@pytest.mark.parametrize("name,fmt", [("e32", "bf16"), ("qwen", "bf16"), ("skew", "bf16"), ("kimi", "bf16"),
+                                      ("kimi", "fp8")])
+def test_full_size_sampled_parity(name, fmt):
     """BASELINE sizes and seeds, forward + backward: routing bit-exact; output
     rows, grad_hidden rows and grad_routing_weights rows of 64 sampled
     tokens (hottest expert, a ragged last tile, spread tokens); the full
     weight gradients of three experts (hottest, median, ragged) -- all
     against the CPU oracle, max relative error <= 2e-2 plus the reference's
     GRAD element check. (E32 is a forward-only config; its backward is
-    checked too.)"""
+    checked too.) The Kimi layer also runs with the FP8 FC1 save, the
+    backward reading the E4M3 values and scales."""
     spec = CASES[name]
     inp = make_inputs(spec, device="cuda", seed=1234)
-    op = _op(spec)
+    op = _op(spec, save_fc1_dtype=fmt)
     x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
     out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
     g = mega_moe.moe_backward_triton(saved, dy)
@@ -168,13 +170,13 @@ def test_full_size_sampled_parity(name):
     print(f"[{name}] probe experts (hottest, median, ragged) = {experts}, rows = "
           f"{[int(ref['counts'][e]) for e in experts]}", flush=True)
     toks = _sample_tokens(ref, spec, (experts[0], experts[2]), 64)
-    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks)
+    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks, save_fc1_dtype=fmt)
     assert_rel(out[toks], sub["out"], 2e-2, f"{name} output rows")
     for key in ("grad_hidden", "grad_routing_weights"):
         assert_rel(g[key][toks], sub[key], 2e-2, f"{name} {key} rows")
         assert cmp_grad(g[key][toks], sub[key], GRAD_RTOL, GRAD_ATOL) == 0, key
     for e in experts:
-        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e)
+        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e, save_fc1_dtype=fmt)
         assert_rel(g["grad_gate_up"][e], dgu, 2e-2, f"{name} grad_gate_up[{e}]")
         assert_rel(g["grad_fc2"][e], dfc2, 2e-2, f"{name} grad_fc2[{e}]")
         assert cmp_grad(g["grad_gate_up"][e], dgu, GRAD_RTOL, GRAD_ATOL) == 0

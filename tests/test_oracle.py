@@ -279,6 +279,25 @@ def test_backward_tokens_equals_full_backward(activation):
     assert sub["grad_routing_weights"][0, 0] == 0          # dropped route
 
 
+@pytest.mark.parametrize("fmt", ["fp16", "fp8"])
+def test_sampled_backward_reads_the_narrow_save(fmt):
+    """With a narrowed FC1 save, backward_tokens / backward_expert over the
+    complete row sets equal the full backward reading the same save."""
+    x, sel, w1, w2, rw, dy = _small_case(seed=8, T=32, H=32, inter=128, E=4, k=2)
+    _, st = O.forward(x, sel, w1, w2, rw, save_fc1_dtype=fmt)
+    g = O.backward(st, dy)
+    full = O.backward_tokens(x, sel, w1, w2, rw, dy, range(x.shape[0]), save_fc1_dtype=fmt)
+    assert torch.equal(full["grad_hidden"], g["grad_hidden"])
+    assert torch.equal(full["grad_routing_weights"], g["grad_routing_weights"])
+    for e in range(4):
+        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e, save_fc1_dtype=fmt)
+        assert torch.equal(dgu, g["grad_gate_up"][e]) and torch.equal(dfc2, g["grad_fc2"][e])
+    # and the narrow save changes the gradients (the format is really applied)
+    if fmt == "fp8":
+        ref16 = O.backward_tokens(x, sel, w1, w2, rw, dy, range(x.shape[0]))
+        assert not torch.equal(ref16["grad_hidden"], full["grad_hidden"])
+
+
 @pytest.mark.parametrize("activation", ["swiglu", "clamp_swiglu"])
 def test_backward_expert_equals_full_backward(activation):
     """backward_expert(e) is the e-th slice of the full weight gradients, bit
