@@ -24,6 +24,11 @@ A restatement, written for this repository, of the reference's algorithm:
               kernels/swiglu_bwd.py:52-83 (scale = the bf16-cast routing
               weight, as the reference's saved recv_weights_sorted), every
               GEMM output rounded to bf16 as the reference's bf16 matmuls are.
+* sampled     backward_tokens / backward_expert: the same forward and
+              backward formulas restricted to chosen tokens (output,
+              grad_hidden, grad_routing_weights rows) or to one expert's
+              weight gradients, so full-size configurations can be checked
+              on the CPU.
 
 Where each function is pinned (tests/test_oracle.py): routing against a
 pure-Python brute-force stable sort plus the reference's invariants
@@ -33,7 +38,9 @@ the backward against torch.autograd of an fp64 restatement of the forward
 (as src/mega_moe/_goldens/backward.py:200-283 cross-checks it); the FP8
 quantizer against the closed-form E4M3 value of every code (round trip,
 ties-to-even at every midpoint, saturation) and its per-group invariants
-(max |q| = 448, error <= half an E4M3 step).
+(max |q| = 448, error <= half an E4M3 step); backward_tokens and
+backward_expert bit for bit against the full backward (all tokens, every
+expert, bf16 and narrowed FC1 saves).
 """
 
 from __future__ import annotations
