@@ -172,7 +172,7 @@ int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows,
  * prow(i) = p_rows[i] if p_rows != NULL else i (same for q). Output bf16
  * [E, N1, N2] contiguous; experts with no rows get zeros. max_rows is the
  * row capacity (an upper bound of offsets[E]); it selects the tiling. When
- * experts average <= 128 rows the output write dominates and a streaming
+ * experts average <= 192 rows the output write dominates and a streaming
  * kernel runs over contiguous operands: gathered ones (p_rows / q_rows) are
  * first permuted into the workspace, which needs
  * mm_wgrad_workspace_bytes(max_rows, E, n1, n2) bytes (a smaller or NULL

@@ -48,6 +48,9 @@ CASES = {
     "qwen": CaseSpec("qwen", 8192, 2048, 768, 128, 8, "softmax_topk", True),
     "kimi": CaseSpec("kimi", 4096, 7168, 2048, 896, 16, "softmax_topk", True),
     "skew": CaseSpec("skew", 16384, 4096, 1536, 32, 8, "zipf", True),
+    # the Kimi-scale layer at the reference's larger per-rank token counts
+    "kimi8k": CaseSpec("kimi8k", 8192, 7168, 2048, 896, 16, "softmax_topk", True),
+    "kimi16k": CaseSpec("kimi16k", 16384, 7168, 2048, 896, 16, "softmax_topk", True),
 }
 
 

@@ -143,7 +143,7 @@ def _probe_experts(counts):
 
 
 @pytest.mark.parametrize("name,fmt", [("e32", "bf16"), ("qwen", "bf16"), ("skew", "bf16"), ("kimi", "bf16"),
-                                      ("kimi", "fp8")])
+                                      ("kimi", "fp8"), ("kimi8k", "bf16")])
 def test_full_size_sampled_parity(name, fmt):
     """BASELINE sizes and seeds, forward + backward: routing bit-exact; output
     rows, grad_hidden rows and grad_routing_weights rows of 64 sampled
@@ -181,6 +181,34 @@ def test_full_size_sampled_parity(name, fmt):
         assert_rel(g["grad_fc2"][e], dfc2, 2e-2, f"{name} grad_fc2[{e}]")
         assert cmp_grad(g["grad_gate_up"][e], dgu, GRAD_RTOL, GRAD_ATOL) == 0
         assert cmp_grad(g["grad_fc2"][e], dfc2, GRAD_RTOL, GRAD_ATOL) == 0
+    del inp, out, saved, g, x, sel, w1, w2, rw, dy
+    torch.cuda.empty_cache()
+
+
+def test_kimi_layer_at_16k_tokens():
+    """The Kimi-scale layer at 16384 tokens (the reference's largest bench
+    size per rank): 262144 routes, so every row offset and output index
+    passes 2^28 elements; forward + backward on sampled tokens and one
+    expert's weight gradients against the oracle."""
+    base = CASES["kimi"]
+    spec = CaseSpec("kimi16k", 16384, base.hidden, base.inter, base.experts, base.top_k, base.routing, True)
+    inp = make_inputs(spec, device="cuda", seed=77)
+    op = _op(spec)
+    x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
+    out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, dy)
+    torch.cuda.synchronize()
+    ref = O.route(sel.cpu().numpy(), spec.experts, spec.top_k)
+    assert saved["route_to_send"].cpu().numpy().tolist() == ref["route_to_send"].tolist()
+    toks = [0, 1, 8191, 8192, 16382, 16383]
+    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks)
+    assert_rel(out[toks], sub["out"], 2e-2, "16k output rows")
+    assert_rel(g["grad_hidden"][toks], sub["grad_hidden"], 2e-2, "16k grad_hidden rows")
+    assert_rel(g["grad_routing_weights"][toks], sub["grad_routing_weights"], 2e-2, "16k grad_rw rows")
+    e = int(sel[16383, 0])                      # an expert whose rows reach the end of the route space
+    dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e)
+    assert_rel(g["grad_gate_up"][e], dgu, 2e-2, "16k grad_gate_up")
+    assert_rel(g["grad_fc2"][e], dfc2, 2e-2, "16k grad_fc2")
     del inp, out, saved, g, x, sel, w1, w2, rw, dy
     torch.cuda.empty_cache()
 
