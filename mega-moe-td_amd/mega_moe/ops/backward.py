@@ -25,7 +25,9 @@ from __future__ import annotations
 
 import torch
 
-from ..runtime.timing import NULL_TIMER
+import os
+
+from ..runtime.timing import NULL_TIMER, StageTimer
 from . import _kernels as K
 from .forward import saved_recompute
 
@@ -62,6 +64,12 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
                   situ_linear_beta=saved["situ_linear_beta"], clamp_limit=saved["clamp_limit"])
 
     tm = saved.get("_stage_timer") or NULL_TIMER
+    # MOE_BWD_STAGE_TIMING=1 (reference ops/backward.py:216-230, 333-347): HIP
+    # events around the stages of this pass, summed into the reference's five
+    # intervals and appended to saved["_bwd_stage_samples"]
+    stage_timing = os.environ.get("MOE_BWD_STAGE_TIMING") == "1"
+    if stage_timing and tm is NULL_TIMER:
+        tm = StageTimer()
     pool = saved.get("_workspaces")
     ws_rows = saved.get("_max_routes") or R
     # step 1: FC2 dgrad, B_e(k=h, n=f) = down[e, h, f]
@@ -106,7 +114,29 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
 
     grads = _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter)
     grads._bind(dy, send_token, offsets, dx)
+    if stage_timing:
+        _record_stage_sample(saved, tm)
     return grads
+
+
+# The reference's five backward intervals and the stages of this build that
+# make them up (its combine_fc1_bwd holds the FC1 dgrad and the top-k reduce).
+_BWD_INTERVALS = (
+    ("dispatch", ("fc2_dgrad",)),
+    ("fc2_wgrad", ("act_recompute", "fc2_wgrad")),
+    ("swiglu", ("swiglu_bwd",)),
+    ("fc1_wgrad", ("fc1_wgrad",)),
+    ("combine", ("fc1_dgrad", "combine_bwd")),
+)
+
+
+def _record_stage_sample(saved, timer):
+    """Append this pass's [dispatch, fc2_wgrad, swiglu, fc1_wgrad, combine]
+    milliseconds to saved["_bwd_stage_samples"] and print them (synchronises)."""
+    last = timer.last_pass()
+    sample = [sum(last.get(s, 0.0) for s in stages) for _, stages in _BWD_INTERVALS]
+    saved.setdefault("_bwd_stage_samples", []).append(sample)
+    print("[bwd-stage] " + " ".join(f"{v:8.3f}" for v in sample), flush=True)
 
 
 class MoEGrads(dict):

@@ -31,7 +31,7 @@ import torch.distributed
 from ..config import MoEForwardConfig
 from ..runtime.routing import MoERoutingPlan, RouteTables, plan_from_tables, route
 from ._saved import MoESaved
-from ..runtime.timing import NULL_TIMER
+from ..runtime.timing import NULL_TIMER, StageTimer
 from . import _kernels as K
 
 # Device-kernel limits (csrc/routing.hip kMaxExperts, csrc/rowops.hip combine slots).
@@ -126,7 +126,9 @@ class FusedMoEForward(torch.nn.Module):
         self._forward_stream = None
         self._device = None
         # optional runtime.timing.StageTimer: HIP events between stages
-        self.stage_timer = None
+        # (MOE_FWD_TIMING=1 attaches one, as the reference's phase stamps are
+        # switched on by that variable, ops/forward.py:1656-1660)
+        self.stage_timer = StageTimer() if os.environ.get("MOE_FWD_TIMING", "0") == "1" else None
         # operator-owned workspaces (routing scratch, tile lists, weight-gradient
         # operand staging), sized for max_tokens_per_rank at the first forward so
         # that they never move afterwards (a captured graph keeps their addresses)

@@ -5,6 +5,8 @@ stage stamps (kernels/common.py:86-130, ops/backward.py:216-347): when a
 ``StageTimer`` is attached to an operator, events are recorded on the launch
 stream between stages and ``summary()`` returns the mean milliseconds of each
 stage over the recorded passes. Without a timer nothing is recorded.
+``MOE_FWD_TIMING=1`` attaches a timer to every new ``FusedMoEForward``;
+``MOE_BWD_STAGE_TIMING=1`` times each backward pass on its own.
 """
 
 from __future__ import annotations
@@ -33,6 +35,14 @@ class StageTimer:
 
     def reset(self):
         self._events.clear()
+
+    def last_pass(self) -> dict:
+        """Milliseconds of each stage's most recent recording (synchronises)."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, a, b in self._events:
+            out[name] = a.elapsed_time(b)
+        return out
 
     def summary(self) -> dict:
         """Mean ms per stage name (synchronises)."""

@@ -410,6 +410,26 @@ def test_backward_function_over_unpacked_weights():
     assert_rel(fc2.grad, ref["grad_fc2"], 2e-2, "dfc2")
 
 
+def test_stage_timing_environment(monkeypatch):
+    """MOE_FWD_TIMING=1 attaches a stage timer to a new operator;
+    MOE_BWD_STAGE_TIMING=1 appends each backward's [dispatch, fc2_wgrad,
+    swiglu, fc1_wgrad, combine] milliseconds to saved["_bwd_stage_samples"]
+    (reference ops/backward.py:216-230, 333-347)."""
+    spec = SMALL[0]
+    inp = make_inputs(spec, device="cuda", seed=9)
+    monkeypatch.setenv("MOE_FWD_TIMING", "1")
+    monkeypatch.setenv("MOE_BWD_STAGE_TIMING", "1")
+    op = _op(spec)
+    assert op.stage_timer is not None
+    op.stage_timer = None                      # the backward then times itself
+    for _ in range(2):
+        out, saved = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"],
+                                return_saved=True)
+        mega_moe.moe_backward_triton(saved, inp["dy"])
+        samples = saved["_bwd_stage_samples"]
+        assert len(samples) == 1 and len(samples[0]) == 5 and all(v > 0 for v in samples[0])
+
+
 def test_stage_timing_sync_finalize():
     from mega_moe.runtime.timing import StageTimer
 
