@@ -142,9 +142,11 @@ def _probe_experts(counts):
     return hottest, median, ragged
 
 
-@pytest.mark.parametrize("name,fmt", [("e32", "bf16"), ("qwen", "bf16"), ("skew", "bf16"), ("kimi", "bf16"),
-                                      ("kimi", "fp8"), ("kimi8k", "bf16")])
-def test_full_size_sampled_parity(name, fmt):
+@pytest.mark.parametrize("name,fmt,activation", [
+    ("e32", "bf16", "swiglu"), ("qwen", "bf16", "swiglu"), ("skew", "bf16", "swiglu"), ("kimi", "bf16", "swiglu"),
+    ("kimi", "fp8", "swiglu"), ("kimi8k", "bf16", "swiglu"), ("qwen", "bf16", "situglu"),
+    ("qwen", "fp16", "clamp_swiglu")])
+def test_full_size_sampled_parity(name, fmt, activation):
     """BASELINE sizes and seeds, forward + backward: routing bit-exact; output
     rows, grad_hidden rows and grad_routing_weights rows of 64 sampled
     tokens (hottest expert, a ragged last tile, spread tokens); the full
@@ -152,10 +154,12 @@ def test_full_size_sampled_parity(name, fmt):
     against the CPU oracle, max relative error <= 2e-2 plus the reference's
     GRAD element check. (E32 is a forward-only config; its backward is
     checked too.) The Kimi layer also runs with the FP8 FC1 save, the
-    backward reading the E4M3 values and scales."""
+    backward reading the E4M3 values and scales, and the Qwen-like layer
+    with the SiTU-GLU and clamped SwiGLU activations."""
     spec = CASES[name]
     inp = make_inputs(spec, device="cuda", seed=1234)
-    op = _op(spec, save_fc1_dtype=fmt)
+    kw = _act_kw(activation)
+    op = _op(spec, activation, save_fc1_dtype=fmt, **{k: v for k, v in kw.items() if k != "activation"})
     x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
     out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
     g = mega_moe.moe_backward_triton(saved, dy)
@@ -170,13 +174,13 @@ def test_full_size_sampled_parity(name, fmt):
     print(f"[{name}] probe experts (hottest, median, ragged) = {experts}, rows = "
           f"{[int(ref['counts'][e]) for e in experts]}", flush=True)
     toks = _sample_tokens(ref, spec, (experts[0], experts[2]), 64)
-    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks, save_fc1_dtype=fmt)
+    sub = O.backward_tokens(x, sel, w1, w2, rw, dy, toks, save_fc1_dtype=fmt, **kw)
     assert_rel(out[toks], sub["out"], 2e-2, f"{name} output rows")
     for key in ("grad_hidden", "grad_routing_weights"):
         assert_rel(g[key][toks], sub[key], 2e-2, f"{name} {key} rows")
         assert cmp_grad(g[key][toks], sub[key], GRAD_RTOL, GRAD_ATOL) == 0, key
     for e in experts:
-        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e, save_fc1_dtype=fmt)
+        dgu, dfc2 = O.backward_expert(x, sel, w1, w2, rw, dy, e, save_fc1_dtype=fmt, **kw)
         assert_rel(g["grad_gate_up"][e], dgu, 2e-2, f"{name} grad_gate_up[{e}]")
         assert_rel(g["grad_fc2"][e], dfc2, 2e-2, f"{name} grad_fc2[{e}]")
         assert cmp_grad(g["grad_gate_up"][e], dgu, GRAD_RTOL, GRAD_ATOL) == 0
