@@ -176,7 +176,9 @@ int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows,
  * kernel runs over contiguous operands: gathered ones (p_rows / q_rows) are
  * first permuted into the workspace, which needs
  * mm_wgrad_workspace_bytes(max_rows, E, n1, n2) bytes (a smaller or NULL
- * workspace selects a slower kernel that gathers in place).
+ * workspace selects a slower kernel that gathers in place). That size
+ * covers every call with at most max_rows rows, so a workspace sized for a
+ * capacity serves all smaller calls.
  * Replaces kernels/transposed_grouped_gemm.py:24-100 and the default
  * torch_npu grouped wgrad of ops/backward.py:85-94.
  */

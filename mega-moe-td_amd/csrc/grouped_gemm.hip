@@ -36,6 +36,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -1052,7 +1053,8 @@ int device_cus() {
 // while the K loop is short: kept up to 192 rows per expert on average
 // (Kimi-scale 8192 tokens, 146 rows: FC1 wgrad 16.3 -> 15.7 ms against the
 // deep-K kernel; 16384 tokens, 292 rows: deep-K 22.9 against 24.7 ms).
-bool wgrad_small_k(int64_t max_rows, int E) { return max_rows <= 192 * static_cast<int64_t>(E); }
+constexpr int64_t kSmallKRows = 192;
+bool wgrad_small_k(int64_t max_rows, int E) { return max_rows <= kSmallKRows * static_cast<int64_t>(E); }
 
 template <int BLAYOUT, int EPI>
 int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* ws, hipStream_t s,
@@ -1179,9 +1181,13 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
   return run_rows<B_NCONTIG, EPI_STORE>(p, offsets, max_rows, num_experts, workspace, s, "mm_grouped_gemm");
 }
 
+// Bytes that any call with at most max_rows rows needs: calls above the
+// small-K bound use the deep-K kernel and no workspace, so the largest need
+// is at min(max_rows, that bound).
 extern "C" size_t mm_wgrad_workspace_bytes(int64_t max_rows, int32_t num_experts, int32_t n1, int32_t n2) {
-  if (max_rows <= 0 || num_experts <= 0 || !wgrad_small_k(max_rows, num_experts)) return 0;
-  return mm_align_up(static_cast<size_t>(max_rows) * n1 * 2, 256) + static_cast<size_t>(max_rows) * n2 * 2;
+  if (max_rows <= 0 || num_experts <= 0) return 0;
+  const int64_t r = std::min<int64_t>(max_rows, kSmallKRows * static_cast<int64_t>(num_experts));
+  return mm_align_up(static_cast<size_t>(r) * n1 * 2, 256) + static_cast<size_t>(r) * n2 * 2;
 }
 
 extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows, const uint16_t* q,

@@ -42,3 +42,16 @@ def test_host_side_argument_errors():
     rc = lib.mm_grouped_gemm(None, 0, None, None, 0, 0, 0, None, 1, 1, 100, 64, None, 0, None, 0, None)
     assert rc == -1
     assert lib.mm_route_workspace_bytes(131072, 896) >= 64 * 896 * 4
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.library_path()), reason="libmegamoe.so not built")
+def test_wgrad_workspace_covers_smaller_calls():
+    """mm_wgrad_workspace_bytes(capacity) covers every call with fewer rows:
+    an operator sized for 16384 tokens (292 Kimi rows per expert, deep-K
+    kernel, no staging) still holds the staging a 4096-token call needs."""
+    lib = _lib.load()
+    E, n1, n2 = 896, 7168, 4096
+    need = [lib.mm_wgrad_workspace_bytes(r, E, n1, n2) for r in (1, 4096 * 16, 8192 * 16, 16384 * 16)]
+    assert need[0] > 0 and need == sorted(need)
+    assert need[3] == need[2] or need[3] >= need[1]
+    assert lib.mm_wgrad_workspace_bytes(4096 * 16, E, n1, n2) >= 4096 * 16 * (n1 + n2) * 2
