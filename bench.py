@@ -41,7 +41,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="kimi",
-                    help="toy | e32 | qwen | kimi | skew | kimi8k | kimi16k (default: kimi fwd+bwd)")
+                    help="toy | e32 | qwen | kimi | skew | kimi8k | kimi16k | dsv3 (default: kimi fwd+bwd)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--save-fc1-dtype", default="bf16", choices=("bf16", "fp16", "fp8"),
                     help="saved FC1 format of the training configs (MoEForwardConfig.save_fc1_dtype)")
@@ -85,7 +85,7 @@ STAGE_KERNELS = {
 # expert (Kimi: 1/16 of the experts and of the tokens, 73 rows per expert as
 # in the full layer); Skew keeps all 32 experts so the Zipf skew is preserved.
 CPU_SAMPLE = {"toy": (512, 8), "e32": (1024, 8), "qwen": (1024, 16), "kimi": (256, 56), "skew": (2048, 32),
-              "kimi8k": (512, 56), "kimi16k": (1024, 56)}
+              "kimi8k": (512, 56), "kimi16k": (1024, 56), "dsv3": (256, 16)}
 
 
 def cpu_inputs(spec, tokens: int, experts: int, seed: int = 99):

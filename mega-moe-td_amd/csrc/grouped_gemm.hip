@@ -986,11 +986,16 @@ int launch_tiles(const int32_t* offsets, int E, int BM, void* ws, hipStream_t s)
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Row-GEMM tile choice: 256x256 when experts average more than 128 rows,
+// Row-GEMM tile choice: 256x256 when experts average at least 96 rows,
 // else a 128-row tile; 256-wide N tiles when N allows. With 129-255 rows per
 // expert one 256-row tile covers an expert, so its weights stream once (two
 // 128-row tiles read them twice: Kimi-scale layer at 8192 tokens, 146 rows
-// per expert, 72.2 -> 63.0 ms per fwd+bwd step).
+// per expert, 72.2 -> 63.0 ms per fwd+bwd step). From an average of 96 rows
+// per expert on, softmax top-k routing puts about half the experts above 128
+// rows, so the 256-row tile already pays (E=256 top-8 at 4096 tokens, 128
+// rows per expert on average: 17.5 -> 16.4 ms per step); below that (Kimi at
+// 4096 tokens, 73 rows) it loses to the 128-row tile (43 -> 48 ms at a
+// threshold of 64).
 struct RowsCfg {
   int bm, bn;
 };
@@ -998,7 +1003,7 @@ struct RowsCfg {
 RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
   RowsCfg c;
   c.bn = (n % 256 == 0) ? 256 : 128;
-  c.bm = (c.bn == 256 && max_rows > 128 * static_cast<int64_t>(E)) ? 256 : 128;
+  c.bm = (c.bn == 256 && max_rows >= 96 * static_cast<int64_t>(E)) ? 256 : 128;
   return c;
 }
 

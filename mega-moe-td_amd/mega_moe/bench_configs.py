@@ -51,6 +51,8 @@ CASES = {
     # the Kimi-scale layer at the reference's larger per-rank token counts
     "kimi8k": CaseSpec("kimi8k", 8192, 7168, 2048, 896, 16, "softmax_topk", True),
     "kimi16k": CaseSpec("kimi16k", 16384, 7168, 2048, 896, 16, "softmax_topk", True),
+    # DeepSeek-V3-like layer: 256 experts, top-8, 128 rows per expert on average
+    "dsv3": CaseSpec("dsv3", 4096, 7168, 2048, 256, 8, "softmax_topk", True),
 }
 
 
