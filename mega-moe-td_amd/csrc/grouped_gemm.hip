@@ -110,6 +110,7 @@ __device__ __forceinline__ void grouped_mn(int l, int num_m, int num_n, int& m, 
 // (which source vector a lane fetches) and undone on the LDS read side.
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void gbl_void;
@@ -185,6 +186,18 @@ struct KcTile {
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + k0, lds + (v * (NT / 64) + wave) * kChunkElems);
   }
+  // Register-staged copy: the same vectors as issue(), loaded into VGPRs now
+  // and written to the same LDS positions by put() later.
+  __device__ void load(u32x4_t (&r)[PER_WAVE], int64_t k0) const {
+#pragma unroll
+    for (int v = 0; v < PER_WAVE; ++v) r[v] = *reinterpret_cast<const u32x4_t*>(ptr[v] + k0);
+  }
+  __device__ static void put(bf16* lds, const u32x4_t (&r)[PER_WAVE]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int v = 0; v < PER_WAVE; ++v)
+      *reinterpret_cast<u32x4_t*>(lds + (v * (NT / 64) + wave) * kChunkElems + lane * 8) = r[v];
+  }
   // MFMA 32x32x16 operand: row r0 + lane%32, k = kk + 8*(lane/32) .. +8
   __device__ static bf16x8 frag(const bf16* lds, int r0, int kk, int lane) {
     const int r = r0 + (lane & 31);
@@ -229,6 +242,16 @@ struct MnTile {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + off, lds + (v * (NT / 64) + wave) * kChunkElems);
+  }
+  __device__ void load(u32x4_t (&r)[PER_WAVE], int64_t off) const {
+#pragma unroll
+    for (int v = 0; v < PER_WAVE; ++v) r[v] = *reinterpret_cast<const u32x4_t*>(ptr[v] + off);
+  }
+  __device__ static void put(bf16* lds, const u32x4_t (&r)[PER_WAVE]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int v = 0; v < PER_WAVE; ++v)
+      *reinterpret_cast<u32x4_t*>(lds + (v * (NT / 64) + wave) * kChunkElems + lane * 8) = r[v];
   }
   // Per-vector source (wgrad): src(v) -> row pointer (column 0 of the tile)
   // for the K row this lane copies in instruction v.
@@ -311,6 +334,22 @@ struct MmaTile {
     }
   }
 
+  // Single 16-deep sub-step pieces for hand-scheduled loops (TRANS layout).
+  template <class ATile, class BTile, int BK_>
+  __device__ static void frags(bf16x8 (&a)[MI], bf16x8 (&b)[NI], const bf16* As, const bf16* Bs, int wm, int wn,
+                               int kk, int lane) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a[i] = ATile::frag(As, wm * TM + i * 32, kk, lane);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) b[j] = BTile::frag(Bs, wn * TN + j * 32, kk, lane);
+  }
+  __device__ void mfmas_t(const bf16x8 (&a)[MI], const bf16x8 (&b)[NI]) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[i], acc[i][j], 0, 0, 0);
+  }
+
   // Tile row of accumulator element r (0..15) of a 32x32 block for `lane`;
   // the column is lane & 31.
   __device__ static int acc_row(int r, int lane) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
@@ -324,7 +363,6 @@ struct MmaTile {
 // Qwen-like weight gradients -3 to -5%; the combine that reads FC2's output
 // next is a few microseconds slower (the rows no longer wait in the
 // memory-side cache).
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void store_out16(void* dst, uint4 v) {
   __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(dst));
@@ -386,7 +424,143 @@ enum { B_KCONTIG = 0, B_NCONTIG = 1 };
 
 // NST-stage ring of LDS buffers: stage s is copied into buffer s % NST while
 // the MFMAs consume stage s - NST + 1; one barrier per K step.
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, int ACT = 0>
+// Epilogue of a row-GEMM tile (LDS-staged, 16-byte stores); the caller
+// has passed a barrier after the tile's last LDS reads.
+// w_pre(it): routing weight of row threadIdx.x / (BN / 16) + it * NT / (BN / 16).
+template <int BM, int BN, int NT, int EPI, int ACT, class Mma, class WFn>
+__device__ __forceinline__ void rows_epilogue(const RowsArgs& p, bf16* smem, const Mma& mma, int row0, int rows,
+                                              int nt, int wm, int wn, int lane, WFn w_pre) {
+  using Out = StageOut<BM, BN, NT>;
+  constexpr int EPI_VPR = BN / 16, EPI_IT = EPI == EPI_GATED ? BM * EPI_VPR / NT : 1;
+  const int n0 = nt * BN;
+  // The accumulators are
+  // transposed (compute<..., true>): each lane stages 4 consecutive columns
+  // of its row with one 8-byte write.
+  const int trow = wm * Mma::TM + (lane & 31);
+  if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+    for (int i = 0; i < Mma::MI; ++i)
+#pragma unroll
+      for (int j = 0; j < Mma::NI; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          Out::put4(smem, trow + i * 32, wn * Mma::TN + j * 32 + Mma::acc_col(g, lane), mma.acc[i][j][4 * g],
+                    mma.acc[i][j][4 * g + 1], mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
+    Out::flush(smem, rows, p.c + static_cast<int64_t>(row0) * p.ldc + n0, p.ldc);
+  } else {
+    // Stage bf16(gate) in LDS columns [0, BN/2) and bf16(up) in [BN/2, BN)
+    // (tile column = output column - jbase), then each thread turns one
+    // 8-column vector of a row into act = bf16(act_fn(gate, up) * w[row]).
+    const int jbase = nt * (BN / 2);
+#pragma unroll
+    for (int i = 0; i < Mma::MI; ++i)
+#pragma unroll
+      for (int jj = 0; jj < Mma::NI; ++jj)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          Out::put4(smem, trow + i * 32,
+                    (jj & 1) * (BN / 2) + wn * (Mma::TN / 2) + (jj >> 1) * 32 + Mma::acc_col(g, lane),
+                    mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1], mma.acc[i][jj][4 * g + 2],
+                    mma.acc[i][jj][4 * g + 3]);
+    __syncthreads();
+    constexpr int VPR = BN / 16;  // 8-column vectors per output row
+    const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
+    // every lane runs every pass (rows past the tile only skip their
+    // stores) so that the 16 lanes of a row can reduce the FP8 group amax
+    static_assert(VPR == EPI_VPR, "epilogue vector split");
+#pragma unroll
+    for (int it = 0; it < EPI_IT; ++it) {
+      const int idx = threadIdx.x + it * NT;
+      const int r = idx / VPR, cv = idx % VPR;
+      const bool valid = r < rows;
+      const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
+      const uint4 uv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + BN / 2 + cv * 8);
+      const int64_t row = row0 + r;
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+      if (valid) {
+        const float wr = w_pre(it);
+        uint32_t ow[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a0 = gated_act(ACT, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
+                                     p.beta, p.lbeta, p.clamp) * wr;
+          const float a1 = gated_act(ACT, __uint_as_float(gw[q] & 0xffff0000u),
+                                     __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
+          ow[q] = pack_bf16x2(a0, a1);
+        }
+        store_out16(p.c + row * p.ldc + jbase + cv * 8, make_uint4(ow[0], ow[1], ow[2], ow[3]));
+      }
+      if (!p.fc1_out) continue;
+      if (p.fc1_fmt == MM_FC1_BF16) {
+        if (valid) {
+          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          store_out16(fo, gv);
+          store_out16(fo + p.inter, uv);
+        }
+      } else if (p.fc1_fmt == MM_FC1_FP16) {
+        uint32_t gh[4], uh[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          gh[q] = pack_f16x2(__uint_as_float(gw[q] << 16), __uint_as_float(gw[q] & 0xffff0000u));
+          uh[q] = pack_f16x2(__uint_as_float(uw[q] << 16), __uint_as_float(uw[q] & 0xffff0000u));
+        }
+        if (valid) {
+          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          store_out16(fo, make_uint4(gh[0], gh[1], gh[2], gh[3]));
+          store_out16(fo + p.inter, make_uint4(uh[0], uh[1], uh[2], uh[3]));
+        }
+      } else if constexpr ((BN / 2) % MM_FC1_SCALE_GROUP == 0) {
+        // FP8: one scale per row per MM_FC1_SCALE_GROUP columns of gate (and
+        // of up); a tile row holds BN / 2 of them, i.e. one or two groups.
+        // The group's 16 consecutive lanes reduce the amax of |bf16 value|
+        // with xor shuffles. (Narrower tiles never see FP8: mm_fc1_swiglu
+        // requires inter % MM_FC1_SCALE_GROUP == 0 for it, which selects
+        // 256- or 512-wide tiles.)
+        constexpr int GV = MM_FC1_SCALE_GROUP / 8;  // lanes per scale group
+        static_assert(VPR % GV == 0, "scale groups tile the row");
+        float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ga = fmaxf(ga, fmaxf(fabsf(__uint_as_float(gw[q] << 16)), fabsf(__uint_as_float(gw[q] & 0xffff0000u))));
+          ua = fmaxf(ua, fmaxf(fabsf(__uint_as_float(uw[q] << 16)), fabsf(__uint_as_float(uw[q] & 0xffff0000u))));
+        }
+#pragma unroll
+        for (int off = 1; off < GV; off <<= 1) {
+          ga = fmaxf(ga, __shfl_xor(ga, off));
+          ua = fmaxf(ua, __shfl_xor(ua, off));
+        }
+        const float gs = ga > 0.0f ? ga : 1.0f, us = ua > 0.0f ? ua : 1.0f;
+        const float gm = kFp8Max / gs, um = kFp8Max / us;
+        uint32_t gq[2] = {0, 0}, uq[2] = {0, 0};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t g0 = f32_to_e4m3fn(__uint_as_float(gw[q] << 16) * gm);
+          const uint32_t g1 = f32_to_e4m3fn(__uint_as_float(gw[q] & 0xffff0000u) * gm);
+          const uint32_t u0 = f32_to_e4m3fn(__uint_as_float(uw[q] << 16) * um);
+          const uint32_t u1 = f32_to_e4m3fn(__uint_as_float(uw[q] & 0xffff0000u) * um);
+          gq[q >> 1] |= (g0 | (g1 << 8)) << ((q & 1) * 16);
+          uq[q >> 1] |= (u0 | (u1 << 8)) << ((q & 1) * 16);
+        }
+        if (valid) {
+          uint8_t* fo = static_cast<uint8_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
+          store_out8(fo, make_uint2(gq[0], gq[1]));
+          store_out8(fo + p.inter, make_uint2(uq[0], uq[1]));
+          if (cv % GV == 0) {
+            const int groups = p.inter / MM_FC1_SCALE_GROUP;
+            float* sc = p.fc1_scale + row * (2 * groups) + (jbase + cv * 8) / MM_FC1_SCALE_GROUP;
+            sc[0] = gs / kFp8Max;
+            sc[groups] = us / kFp8Max;
+          }
+        }
+      }
+    }
+  }
+}
+
+// REG: operands are loaded into VGPRs one stage ahead and written to a
+// 2-deep LDS ring with ordinary LDS stores after each stage's MFMAs (one
+// barrier per K step), instead of LDS-DMA copies.
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, int ACT = 0, bool REG = false>
 __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   constexpr int WN = 2, WM = NT / 64 / WN;  // 4 waves: 2x2, 8 waves: 4x2
   using Mma = MmaTile<BM, BN, WM, WN>;
@@ -464,6 +638,75 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
       w_pre[it] = r < rows ? p.w[row0 + r] : 0.0f;
     }
   }
+  if constexpr (REG) {
+    static_assert(NST == 2, "register staging uses a 2-deep LDS ring");
+    u32x4_t ra[ATile::PER_WAVE], rb[BTile::PER_WAVE];
+    auto gload = [&](int s) {
+      la.load(ra, static_cast<int64_t>(s) * BK_);
+      lb.load(rb, s * b_step);
+    };
+    auto sput = [&](int s) {
+      bf16* buf = smem + (s & 1) * STAGE;
+      ATile::put(buf, ra);
+      BTile::put(buf + ATile::ELEMS, rb);
+    };
+    static_assert(BK_ == 64, "four 16-deep sub-steps per stage");
+    using Frag = bf16x8;
+    Frag fa[2][Mma::MI], fb[2][Mma::NI];
+    if (nk > 0) {
+      gload(0);
+      sput(0);
+      if (nk > 1) gload(1);
+    }
+    __syncthreads();
+    if (active) {
+      Mma::template frags<ATile, BTile, BK_>(fa[0], fb[0], smem, smem + ATile::ELEMS, wm, wn, 0, lane);
+      // Sub-step s issues its MFMAs from fragment set s & 1 while the next
+      // sub-step's fragments load into the other set. Stage kt + 1's
+      // registers go to LDS during sub-steps 0 (A) and 1 (B), into the slot
+      // stage kt - 1 used (its last fragments were read before the previous
+      // barrier), then stage kt + 2's loads are issued. The barrier after
+      // sub-step 2 publishes stage kt + 1, whose first fragments are read
+      // during sub-step 3.
+      // Branch-free so that the scheduler can interleave the LDS writes and
+      // global loads with the MFMAs: past the last stage the writes land in
+      // a slot nobody reads again and the loads repeat the last stage.
+      for (int kt = 0; kt < nk; ++kt) {
+        const bf16* cur = smem + (kt & 1) * STAGE;
+        bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
+#pragma unroll
+        for (int ss = 0; ss < 4; ++ss) {
+          const int c = ss & 1, n = c ^ 1;
+          if (ss < 3)
+            Mma::template frags<ATile, BTile, BK_>(fa[n], fb[n], cur, cur + ATile::ELEMS, wm, wn, (ss + 1) * 16, lane);
+          else
+            Mma::template frags<ATile, BTile, BK_>(fa[n], fb[n], nxt, nxt + ATile::ELEMS, wm, wn, 0, lane);
+          mma.mfmas_t(fa[c], fb[c]);
+          if (ss == 0) ATile::put(nxt, ra);
+          if (ss == 1) {
+            BTile::put(nxt + ATile::ELEMS, rb);
+            gload(min(kt + 2, nk - 1));
+          }
+#pragma unroll
+          for (int q = 0; q < Mma::MI * Mma::NI; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+          }
+          if (ss == 2) __syncthreads();
+        }
+      }
+    } else {
+      for (int kt = 0; kt < nk; ++kt) {
+        if (kt + 1 < nk) {
+          sput(kt + 1);
+          if (kt + 2 < nk) gload(kt + 2);
+        }
+        __syncthreads();
+      }
+    }
+  } else {
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s)
     if (s < nk) issue(s);
@@ -482,130 +725,10 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
       if (kt + NST - 1 < nk) issue(kt + NST - 1);
     }
   }
+  }
   __syncthreads();
 
-  // ---- epilogue (LDS-staged, 16-byte stores). The accumulators are
-  // transposed (compute<..., true>): each lane stages 4 consecutive columns
-  // of its row with one 8-byte write.
-  const int trow = wm * Mma::TM + (lane & 31);
-  if constexpr (EPI == EPI_STORE) {
-#pragma unroll
-    for (int i = 0; i < Mma::MI; ++i)
-#pragma unroll
-      for (int j = 0; j < Mma::NI; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          Out::put4(smem, trow + i * 32, wn * Mma::TN + j * 32 + Mma::acc_col(g, lane), mma.acc[i][j][4 * g],
-                    mma.acc[i][j][4 * g + 1], mma.acc[i][j][4 * g + 2], mma.acc[i][j][4 * g + 3]);
-    Out::flush(smem, rows, p.c + static_cast<int64_t>(row0) * p.ldc + n0, p.ldc);
-  } else {
-    // Stage bf16(gate) in LDS columns [0, BN/2) and bf16(up) in [BN/2, BN)
-    // (tile column = output column - jbase), then each thread turns one
-    // 8-column vector of a row into act = bf16(act_fn(gate, up) * w[row]).
-    const int jbase = nt * (BN / 2);
-#pragma unroll
-    for (int i = 0; i < Mma::MI; ++i)
-#pragma unroll
-      for (int jj = 0; jj < Mma::NI; ++jj)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          Out::put4(smem, trow + i * 32,
-                    (jj & 1) * (BN / 2) + wn * (Mma::TN / 2) + (jj >> 1) * 32 + Mma::acc_col(g, lane),
-                    mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1], mma.acc[i][jj][4 * g + 2],
-                    mma.acc[i][jj][4 * g + 3]);
-    __syncthreads();
-    constexpr int VPR = BN / 16;  // 8-column vectors per output row
-    const int64_t ldf = 2 * static_cast<int64_t>(p.inter);
-    // every lane runs every pass (rows past the tile only skip their
-    // stores) so that the 16 lanes of a row can reduce the FP8 group amax
-    static_assert(VPR == EPI_VPR, "epilogue vector split");
-#pragma unroll
-    for (int it = 0; it < EPI_IT; ++it) {
-      const int idx = threadIdx.x + it * NT;
-      const int r = idx / VPR, cv = idx % VPR;
-      const bool valid = r < rows;
-      const uint4 gv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + cv * 8);
-      const uint4 uv = *reinterpret_cast<const uint4*>(smem + r * Out::PITCH + BN / 2 + cv * 8);
-      const int64_t row = row0 + r;
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-      if (valid) {
-        const float wr = w_pre[it];
-        uint32_t ow[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float a0 = gated_act(ACT, __uint_as_float(gw[q] << 16), __uint_as_float(uw[q] << 16),
-                                     p.beta, p.lbeta, p.clamp) * wr;
-          const float a1 = gated_act(ACT, __uint_as_float(gw[q] & 0xffff0000u),
-                                     __uint_as_float(uw[q] & 0xffff0000u), p.beta, p.lbeta, p.clamp) * wr;
-          ow[q] = pack_bf16x2(a0, a1);
-        }
-        store_out16(p.c + row * p.ldc + jbase + cv * 8, make_uint4(ow[0], ow[1], ow[2], ow[3]));
-      }
-      if (!p.fc1_out) continue;
-      if (p.fc1_fmt == MM_FC1_BF16) {
-        if (valid) {
-          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
-          store_out16(fo, gv);
-          store_out16(fo + p.inter, uv);
-        }
-      } else if (p.fc1_fmt == MM_FC1_FP16) {
-        uint32_t gh[4], uh[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          gh[q] = pack_f16x2(__uint_as_float(gw[q] << 16), __uint_as_float(gw[q] & 0xffff0000u));
-          uh[q] = pack_f16x2(__uint_as_float(uw[q] << 16), __uint_as_float(uw[q] & 0xffff0000u));
-        }
-        if (valid) {
-          uint16_t* fo = static_cast<uint16_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
-          store_out16(fo, make_uint4(gh[0], gh[1], gh[2], gh[3]));
-          store_out16(fo + p.inter, make_uint4(uh[0], uh[1], uh[2], uh[3]));
-        }
-      } else if constexpr ((BN / 2) % MM_FC1_SCALE_GROUP == 0) {
-        // FP8: one scale per row per MM_FC1_SCALE_GROUP columns of gate (and
-        // of up); a tile row holds BN / 2 of them, i.e. one or two groups.
-        // The group's 16 consecutive lanes reduce the amax of |bf16 value|
-        // with xor shuffles. (Narrower tiles never see FP8: mm_fc1_swiglu
-        // requires inter % MM_FC1_SCALE_GROUP == 0 for it, which selects
-        // 256- or 512-wide tiles.)
-        constexpr int GV = MM_FC1_SCALE_GROUP / 8;  // lanes per scale group
-        static_assert(VPR % GV == 0, "scale groups tile the row");
-        float ga = 0.0f, ua = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          ga = fmaxf(ga, fmaxf(fabsf(__uint_as_float(gw[q] << 16)), fabsf(__uint_as_float(gw[q] & 0xffff0000u))));
-          ua = fmaxf(ua, fmaxf(fabsf(__uint_as_float(uw[q] << 16)), fabsf(__uint_as_float(uw[q] & 0xffff0000u))));
-        }
-#pragma unroll
-        for (int off = 1; off < GV; off <<= 1) {
-          ga = fmaxf(ga, __shfl_xor(ga, off));
-          ua = fmaxf(ua, __shfl_xor(ua, off));
-        }
-        const float gs = ga > 0.0f ? ga : 1.0f, us = ua > 0.0f ? ua : 1.0f;
-        const float gm = kFp8Max / gs, um = kFp8Max / us;
-        uint32_t gq[2] = {0, 0}, uq[2] = {0, 0};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t g0 = f32_to_e4m3fn(__uint_as_float(gw[q] << 16) * gm);
-          const uint32_t g1 = f32_to_e4m3fn(__uint_as_float(gw[q] & 0xffff0000u) * gm);
-          const uint32_t u0 = f32_to_e4m3fn(__uint_as_float(uw[q] << 16) * um);
-          const uint32_t u1 = f32_to_e4m3fn(__uint_as_float(uw[q] & 0xffff0000u) * um);
-          gq[q >> 1] |= (g0 | (g1 << 8)) << ((q & 1) * 16);
-          uq[q >> 1] |= (u0 | (u1 << 8)) << ((q & 1) * 16);
-        }
-        if (valid) {
-          uint8_t* fo = static_cast<uint8_t*>(p.fc1_out) + row * ldf + jbase + cv * 8;
-          store_out8(fo, make_uint2(gq[0], gq[1]));
-          store_out8(fo + p.inter, make_uint2(uq[0], uq[1]));
-          if (cv % GV == 0) {
-            const int groups = p.inter / MM_FC1_SCALE_GROUP;
-            float* sc = p.fc1_scale + row * (2 * groups) + (jbase + cv * 8) / MM_FC1_SCALE_GROUP;
-            sc[0] = gs / kFp8Max;
-            sc[groups] = us / kFp8Max;
-          }
-        }
-      }
-    }
-  }
+  rows_epilogue<BM, BN, NT, EPI, ACT>(p, smem, mma, row0, rows, nt, wm, wn, lane, [&](int it) { return w_pre[it]; });
 }
 
 // ------------------------------------------------------------------ wgrad
@@ -743,12 +866,13 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
   }
 }
 
+__device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
+
 // ------------------------------------------------------------------ small-K wgrad
 //
 // Weight gradient when experts hold few rows (K of the GEMM; e.g. 73 rows
 // per expert at 4096 tokens, top-16 over 896 experts): the E x n1 x n2 bf16
 // output write dominates.
-__device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
 
 // Two consecutive int32 at a wave-uniform address, loaded through the scalar
 // cache (completion tracked by lgkmcnt, not vmcnt).
@@ -1007,27 +1131,26 @@ RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
   return c;
 }
 
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads>
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, bool REG = false>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
   if constexpr (EPI == EPI_GATED) {  // activation specialised at compile time
     if (p.act_kind == MM_ACT_SWIGLU)
-      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SWIGLU><<<grid, NT, 0, s>>>(p);
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SWIGLU, REG><<<grid, NT, 0, s>>>(p);
     else if (p.act_kind == MM_ACT_CLAMP_SWIGLU)
-      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_CLAMP_SWIGLU><<<grid, NT, 0, s>>>(p);
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_CLAMP_SWIGLU, REG><<<grid, NT, 0, s>>>(p);
     else
-      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SITUGLU><<<grid, NT, 0, s>>>(p);
+      grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SITUGLU, REG><<<grid, NT, 0, s>>>(p);
   } else {
-    grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT><<<grid, NT, 0, s>>>(p);
+    grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, 0, REG><<<grid, NT, 0, s>>>(p);
   }
 }
 
-// 8 waves (2 per SIMD) per 256x256 and 128x256 workgroup by default: a
-// second wave on each SIMD keeps the matrix core busy across the other's
-// LDS waits and barriers (measured +10% over 4 waves on 256-row tiles, -7%
-// time on the 128-row tiles of small experts). MM_GEMM_WAVES=4 selects 4
-// waves.
+// 8 waves (2 per SIMD) per 128x256 workgroup by default: a second wave on
+// each SIMD keeps the matrix core busy across the other's LDS waits and
+// barriers (-7% time on the 128-row tiles of small experts against 4
+// waves). MM_GEMM_WAVES=4 selects 4 waves.
 int eight_waves() {
   static int v = -1;
   if (v < 0) {
@@ -1035,6 +1158,22 @@ int eight_waves() {
     v = (e && strcmp(e, "4") == 0) ? 0 : 1;
   }
   return v;
+}
+
+// 256x256 row tiles with K >= 1024: 4 waves of 128x128 with register-staged
+// operand copies (one wave per SIMD, 2/3 of the LDS fragment traffic of 8
+// waves of 64x128; the next stage's LDS writes and the following stage's
+// global loads interleaved with the MFMAs): E32 and Skew layer steps -3%,
+// the K-contiguous dgrads -4 to -7%, against 8 waves with LDS-DMA copies,
+// which run the shorter K loops (Qwen-like FC2, K = 768: 0.271 against
+// 0.280 ms) and which MM_ROWS_DMA=1 selects everywhere.
+bool rows_lds_dma() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("MM_ROWS_DMA");
+    v = (e && strcmp(e, "1") == 0) ? 1 : 0;
+  }
+  return v == 1;
 }
 
 enum { WG_WIDE = 0, WG_TILE = 1, WG_LARGE = 2 };
@@ -1072,10 +1211,10 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   // (Kimi-scale: -5% layer time against 8-deep groups)
   p.group_m = c.bm == 128 ? 1 : GROUP_M;
   if (c.bm == 256) {
-    if (eight_waves())
+    if (rows_lds_dma() || p.k < 1024)
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
     else
-      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI>(p, max_rows, E, s);
+      launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 256, true>(p, max_rows, E, s);
   } else if (c.bn == 256) {
     // Weight streaming with N-contiguous weights (FC1, FC2 of small
     // experts): 512-wide tiles halve the tile count and with it the per-tile
@@ -1257,10 +1396,7 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   if (small) {
     grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256 && bn == 256) {
-    if (eight_waves())
-      grouped_wgrad_kernel<256, 256, 64, 2, false, 512><<<grid, 512, 0, s>>>(a, num_experts, px);
-    else
-      grouped_wgrad_kernel<256, 256, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
+    grouped_wgrad_kernel<256, 256, 64, 2, false, 512><<<grid, 512, 0, s>>>(a, num_experts, px);
   } else if (bm == 256) {
     grouped_wgrad_kernel<256, 128, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bn == 256) {
