@@ -145,7 +145,7 @@ def _probe_experts(counts):
 @pytest.mark.parametrize("name,fmt,activation", [
     ("e32", "bf16", "swiglu"), ("qwen", "bf16", "swiglu"), ("skew", "bf16", "swiglu"), ("kimi", "bf16", "swiglu"),
     ("kimi", "fp8", "swiglu"), ("kimi8k", "bf16", "swiglu"), ("qwen", "bf16", "situglu"),
-    ("qwen", "fp16", "clamp_swiglu")])
+    ("qwen", "fp16", "clamp_swiglu"), ("qwen", "fp8", "swiglu"), ("dsv3", "bf16", "swiglu")])
 def test_full_size_sampled_parity(name, fmt, activation):
     """BASELINE sizes and seeds, forward + backward: routing bit-exact; output
     rows, grad_hidden rows and grad_routing_weights rows of 64 sampled
@@ -154,8 +154,10 @@ def test_full_size_sampled_parity(name, fmt, activation):
     against the CPU oracle, max relative error <= 2e-2 plus the reference's
     GRAD element check. (E32 is a forward-only config; its backward is
     checked too.) The Kimi layer also runs with the FP8 FC1 save, the
-    backward reading the E4M3 values and scales, and the Qwen-like layer
-    with the SiTU-GLU and clamped SwiGLU activations."""
+    backward reading the E4M3 values and scales (128-row tiles), the
+    Qwen-like layer with the SiTU-GLU and clamped SwiGLU activations and the
+    FP8 save (256-row register-staged tiles), and the DeepSeek-V3-like layer
+    (256 experts averaging 128 rows, 256-row tiles)."""
     spec = CASES[name]
     inp = make_inputs(spec, device="cuda", seed=1234)
     kw = _act_kw(activation)
