@@ -32,6 +32,34 @@ from . import _kernels as K
 from .forward import saved_recompute
 
 
+# Step 2 overlaps step 3 when experts average more route-capacity rows than
+# this: the FC2 weight gradient is then a long MFMA-bound launch (Skew-like
+# layer, 4096 rows per expert: step 14.85 -> 14.74 ms). At 512 rows (Qwen-like)
+# the two launches are short and the overlap measured 0.6% slower; at 192 rows
+# or fewer the weight gradient streams its output and is itself HBM-bound.
+_OVERLAP_ROWS = 1024
+_SIDE_STREAMS: dict = {}
+
+
+def overlap_act_bwd(num_routes: int, num_experts: int) -> bool:
+    """Whether step 2 runs on a second stream beside step 3: by default when
+    experts average more than 1024 route-capacity rows;
+    ``MM_BWD_ACT_OVERLAP=0`` / ``=1`` forces it off / on."""
+    env = os.environ.get("MM_BWD_ACT_OVERLAP")
+    if env in ("0", "1"):
+        return env == "1"
+    return num_routes > _OVERLAP_ROWS * num_experts
+
+
+def _side_stream(device) -> torch.cuda.Stream:
+    key = str(device)
+    st = _SIDE_STREAMS.get(key)
+    if st is None:
+        st = torch.cuda.Stream(device=device)  # default priority
+        _SIDE_STREAMS[key] = st
+    return st
+
+
 def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_states=None):
     """Run the five backward stages on a ``saved`` dict from ``FusedMoEForward``.
 
@@ -78,16 +106,35 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     grad_act = K.grouped_gemm(dy, send_token, w2, se, sf, sh, offsets, R, inter, H, pool=pool)
     tm.end()
     # step 2: gated-activation backward
-    tm.begin("swiglu_bwd")
+    side = _side_stream(dy.device) if overlap_act_bwd(R, offsets.numel() - 1) else None
+    if side is None:  # overlapped with step 3 otherwise: its time is part of "fc2_wgrad"
+        tm.begin("swiglu_bwd")
     fc1_scale = None
     if saved["fc1_output"].dtype == torch.float8_e4m3fn:
         # FP8 save: dequantize at the load (reference kernels/mega_bwd.py:3185-3206)
         fc1_scale = saved.get("fc1_output_scale")
         if fc1_scale is None or int(saved.get("fc1_scale_group_size", 0)) != 128:
             raise ValueError("an FP8 fc1_output needs fc1_output_scale with fc1_scale_group_size 128")
-    dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
-                               fc1_scale=fc1_scale, **act_kw)
-    tm.end()
+    if side is None:
+        dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
+                                   fc1_scale=fc1_scale, **act_kw)
+    else:
+        # step 2 (HBM-bound, no LDS) on a second stream beside step 3 (the
+        # MFMA-bound deep-K weight gradient): its waves fit in the register
+        # and LDS space the GEMM's one workgroup per CU leaves free (the
+        # reference's step 2 || step 3, ops/backward.py:241-271)
+        main = torch.cuda.current_stream(dy.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
+                                       fc1_scale=fc1_scale, **act_kw)
+        for t in (grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, fc1_scale):
+            if t is not None:
+                t.record_stream(side)
+        dab.record_stream(main)
+        dscale.record_stream(main)
+    if side is None:
+        tm.end()
     # step 3: FC2 wgrad  dW2[e][h, f] = sum_i gco[i, h] act[i, f]
     act = saved.get("swiglu_out_weighted")
     if act is None or saved_recompute():
@@ -98,6 +145,8 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
         tm.end()
     tm.begin("fc2_wgrad")
     grad_fc2 = K.grouped_wgrad(dy, send_token, act, None, offsets, H, inter, pool=pool, ws_rows=ws_rows)
+    if side is not None:
+        main.wait_stream(side)
     tm.end()
     # step 4: FC1 dgrad, B_e(k=j, n=h) = W1[e, h, j]; top-k reduce; gate gather
     tm.begin("fc1_dgrad")

@@ -6,7 +6,8 @@ The path makes no host synchronisation and records no memset nodes: routing
 counts, tile lists and every output are written by kernels, so a caller can
 capture a training step. The operator is single-stream (the reference's
 rule, forward.py:1929-1936), so the eager warm-up and the capture run on the
-same side stream. Replays alternate with eager work on the same tensors and
+same side stream; the backward's own fork of the activation backward onto a
+second stream (and its join) is captured with it. Replays alternate with eager work on the same tensors and
 with new inputs copied into the captured ones.
 """
 
@@ -31,7 +32,11 @@ def _step(op, inp):
     CaseSpec("graph_small", 256, 256, 256, 8, 4, "softmax_topk", True),
     CaseSpec("graph_wide", 512, 1024, 512, 16, 2, "zipf", True),
 ], ids=lambda s: s.name)
-def test_captured_step_replays_bit_exact(spec):
+@pytest.mark.parametrize("overlap", ["0", "1"])
+def test_captured_step_replays_bit_exact(spec, overlap, monkeypatch):
+    # overlap=1: the activation backward forks onto a second stream and joins
+    # before the FC1 dgrad, inside the capture
+    monkeypatch.setenv("MM_BWD_ACT_OVERLAP", overlap)
     inp = make_inputs(spec, device="cuda", seed=5, weight_scale=0.1)
     alt = make_inputs(spec, device="cuda", seed=6, weight_scale=0.1)
     cfg = mega_moe.MoEForwardConfig()

@@ -441,6 +441,35 @@ def test_backward_function_over_unpacked_weights():
     assert_rel(fc2.grad, ref["grad_fc2"], 2e-2, "dfc2")
 
 
+@pytest.mark.parametrize("spec", [SMALL[1], CaseSpec("overlap_deep_k", 1024, 512, 256, 8, 4, "zipf", True)],
+                         ids=lambda s: s.name)
+@pytest.mark.parametrize("fmt", ["bf16", "fp8"])
+def test_act_backward_overlap_is_bit_identical(spec, fmt, monkeypatch):
+    """Step 2 on a second stream beside step 3 (MM_BWD_ACT_OVERLAP=1, the
+    default above 1024 rows per expert) gives the same bits
+    as the one-stream order, and the side stream's outputs are complete when
+    the backward returns (the FC1 dgrad waits for them)."""
+    inp = make_inputs(spec, device="cuda", seed=21)
+    op = _op(spec, save_fc1_dtype=fmt)
+    got = {}
+    for ov in ("0", "1", "0"):
+        monkeypatch.setenv("MM_BWD_ACT_OVERLAP", ov)
+        out, saved = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"],
+                                return_saved=True)
+        g = mega_moe.moe_backward_triton(saved, inp["dy"])
+        del saved                                   # the side stream's inputs may be released at once
+        scratch = torch.randn(1 << 22, device="cuda")  # allocations right after must not disturb it
+        vals = {k: g[k].clone() for k in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up",
+                                           "grad_fc1_output", "grad_gate")}
+        del scratch
+        if ov in got:
+            for k, v in vals.items():
+                assert torch.equal(v, got[ov][k]), k
+        got[ov] = vals
+    for k in got["0"]:
+        assert torch.equal(got["0"][k], got["1"][k]), f"{k} differs with the overlapped activation backward"
+
+
 def test_stage_timing_environment(monkeypatch):
     """MOE_FWD_TIMING=1 attaches a stage timer to a new operator;
     MOE_BWD_STAGE_TIMING=1 appends each backward's [dispatch, fc2_wgrad,
