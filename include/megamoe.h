@@ -207,6 +207,20 @@ int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_to_send,
                uint16_t* out, int64_t ldo, mm_stream_t stream);
 
 /*
+ * Backward top-k reduce and routing-weight gradient gather in one launch:
+ *   grad_hidden = mm_combine(dx, route_to_send)  and
+ *   grad_rw[r]  = float(dscale[route_to_send[r]]) or 0 for dropped routes,
+ * the two outputs of mm_combine + mm_gather_route_grad on the FC1 dgrad rows.
+ * Replaces the grad_hidden reduce and gate-channel gather of
+ * kernels/combine_fc1_bwd.py:357-394.
+ */
+int mm_combine_bwd(const uint16_t* dx, int64_t ldx,
+                   const int32_t* route_to_send, int64_t num_tokens,
+                   int32_t top_k, int32_t hidden, uint16_t* grad_hidden,
+                   int64_t ldo, const uint16_t* dscale, float* grad_rw,
+                   mm_stream_t stream);
+
+/*
  * Gather of the per-row routing-weight gradient back to [T, k] order:
  *   grad_rw[r] = float(dscale[route_to_send[r]]) or 0 for dropped routes.
  * Replaces the gate-channel gather of kernels/combine_fc1_bwd.py:357-394.

@@ -85,14 +85,20 @@ __global__ __launch_bounds__(kThreads) void combine_items_kernel(const uint4* __
                                                                  const int32_t* __restrict__ route_to_send,
                                                                  int64_t T, int top_k, int hidden_v,
                                                                  uint4* __restrict__ out, int64_t ldo_v,
-                                                                 int nchunks) {
+                                                                 int nchunks, const uint16_t* __restrict__ dscale,
+                                                                 float* __restrict__ grad_rw) {
   const int lane = threadIdx.x & 63;
   const int64_t items = T * nchunks;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6); w < items;
        w += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
     const int64_t t = w / nchunks;
-    const int v0 = static_cast<int>(w % nchunks) * 64 * VPL + lane;
+    const int chunk = static_cast<int>(w % nchunks);
+    const int v0 = chunk * 64 * VPL + lane;
     const int my_row = lane < top_k ? route_to_send[t * top_k + lane] : -1;
+    // backward: the token's chunk-0 wavefront also gathers the routing-weight
+    // gradient of its k slots (0 for dropped routes)
+    if (grad_rw && chunk == 0 && lane < top_k)
+      grad_rw[t * top_k + lane] = my_row >= 0 ? bf16_bits_to_f32(dscale[my_row]) : 0.0f;
     float acc[VPL][8];
 #pragma unroll
     for (int u = 0; u < VPL; ++u)
@@ -337,21 +343,40 @@ extern "C" int mm_permute(const uint16_t* x, int64_t ldx, const int32_t* send_to
   return mm_check_launch("mm_permute");
 }
 
-extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_to_send, int64_t num_tokens,
-                          int32_t top_k, int32_t hidden, uint16_t* out, int64_t ldo, mm_stream_t stream) {
-  MM_CHECK_ARG(num_tokens >= 0 && hidden > 0, "mm_combine: bad sizes");
-  MM_CHECK_ARG(top_k > 0 && top_k <= 64, "mm_combine: top_k must be in [1, 64]");
+namespace {
+
+int launch_combine(const uint16_t* y, int64_t ldy, const int32_t* route_to_send, int64_t num_tokens,
+                   int32_t top_k, int32_t hidden, uint16_t* out, int64_t ldo, const uint16_t* dscale,
+                   float* grad_rw, mm_stream_t stream, const char* what) {
+  MM_CHECK_ARG(num_tokens >= 0 && hidden > 0, "%s: bad sizes", what);
+  MM_CHECK_ARG(top_k > 0 && top_k <= 64, "%s: top_k must be in [1, 64]", what);
   if (num_tokens == 0) return MM_OK;
-  MM_CHECK_ARG(y && route_to_send && out, "mm_combine: null pointer");
+  MM_CHECK_ARG(y && route_to_send && out, "%s: null pointer", what);
   MM_CHECK_ARG(hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) && aligned16(out),
-               "mm_combine: rows must be 16-byte aligned");
+               "%s: rows must be 16-byte aligned", what);
   const int nchunks = (hidden / 8 + 127) / 128;
   int64_t g = (num_tokens * nchunks + kRowsPerBlock - 1) / kRowsPerBlock;
   if (g > 65536) g = 65536;
   combine_items_kernel<2, 8><<<static_cast<int>(g), kThreads, 0, mm_hip_stream(stream)>>>(
       reinterpret_cast<const uint4*>(y), ldy / 8, route_to_send, num_tokens, top_k, hidden / 8,
-      reinterpret_cast<uint4*>(out), ldo / 8, nchunks);
-  return mm_check_launch("mm_combine");
+      reinterpret_cast<uint4*>(out), ldo / 8, nchunks, dscale, grad_rw);
+  return mm_check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int mm_combine(const uint16_t* y, int64_t ldy, const int32_t* route_to_send, int64_t num_tokens,
+                          int32_t top_k, int32_t hidden, uint16_t* out, int64_t ldo, mm_stream_t stream) {
+  return launch_combine(y, ldy, route_to_send, num_tokens, top_k, hidden, out, ldo, nullptr, nullptr, stream,
+                        "mm_combine");
+}
+
+extern "C" int mm_combine_bwd(const uint16_t* dx, int64_t ldx, const int32_t* route_to_send, int64_t num_tokens,
+                              int32_t top_k, int32_t hidden, uint16_t* grad_hidden, int64_t ldo,
+                              const uint16_t* dscale, float* grad_rw, mm_stream_t stream) {
+  MM_CHECK_ARG(num_tokens == 0 || (dscale && grad_rw), "mm_combine_bwd: null pointer");
+  return launch_combine(dx, ldx, route_to_send, num_tokens, top_k, hidden, grad_hidden, ldo, dscale, grad_rw,
+                        stream, "mm_combine_bwd");
 }
 
 extern "C" int mm_gather_route_grad(const uint16_t* dscale, const int32_t* route_to_send, int64_t num_routes,

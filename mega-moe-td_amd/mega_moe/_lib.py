@@ -46,6 +46,7 @@ SIGNATURES = {
                                         _SZ, _P]),
     "mm_combine": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _I32, _P, _I64, _P]),
     "mm_gather_route_grad": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
+    "mm_combine_bwd": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _I32, _P, _I64, _P, _P, _P]),
     "mm_gated_act": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I64, _I32, _I32, _F32, _F32, _F32, _P,
                                     _I64, _P]),
     "mm_swiglu_bwd": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _P, _P, _P, _I32, _I64, _I32, _I32, _F32,

@@ -180,6 +180,18 @@ def combine(y, route_to_send, num_tokens: int, top_k: int) -> torch.Tensor:
     return out
 
 
+def combine_bwd(dx, route_to_send, num_tokens: int, top_k: int, dscale):
+    """(grad_hidden [T, H] bf16, grad_rw [T, k] fp32) in one launch: the top-k
+    reduce of dx and the gather of dscale to the routes (0 where dropped)."""
+    _check_bf16("dx", dx)
+    hidden = dx.shape[1]
+    gh = torch.empty(num_tokens, hidden, dtype=torch.bfloat16, device=dx.device)
+    grw = torch.empty(num_tokens, top_k, dtype=torch.float32, device=dx.device)
+    _lib.call("mm_combine_bwd", _lib.ptr(dx), dx.stride(0), _lib.ptr(route_to_send), num_tokens, top_k, hidden,
+              _lib.ptr(gh), gh.stride(0), _lib.ptr(dscale), _lib.ptr(grw), _lib.stream_of(dx.device))
+    return gh, grw
+
+
 def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str, situ_beta: float,
                situ_linear_beta, clamp_limit: float, fc1_scale=None):
     """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16).

@@ -153,8 +153,7 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     dx = K.grouped_gemm(dab, None, w1, w1.stride(0), w1.stride(1), 1, offsets, R, H, 2 * inter, pool=pool)
     tm.end()
     tm.begin("combine_bwd")
-    grad_hidden = K.combine(dx, r2s, T, k)
-    grad_rw = K.gather_route_grad(dscale, r2s, (T, k))
+    grad_hidden, grad_rw = K.combine_bwd(dx, r2s, T, k, dscale)
     tm.end()
     # step 5: FC1 wgrad in the packed layout  dW1[e][h, j] = sum_i x[tok(i), h] dAB[i, j]
     tm.begin("fc1_wgrad")

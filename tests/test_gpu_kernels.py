@@ -246,3 +246,24 @@ def test_swiglu_bwd(activation, fmt):
     ref_ds = (act_a * v * gaf).sum(1)
     assert_rel(dab[:290], ref_dab, 1e-2, "dab")
     assert_rel(ds[:290], ref_ds, 1e-2, "dscale")
+
+
+@pytest.mark.parametrize("T,k,H", [(300, 6, 384), (129, 16, 7168), (1, 1, 128)])
+def test_combine_bwd_one_launch(T, k, H):
+    """mm_combine_bwd = mm_combine + mm_gather_route_grad in one launch: the
+    top-k reduce exact on integer rows, grad_rw gathered from dscale with 0
+    for dropped routes, both equal to the two-launch results."""
+    from mega_moe.ops import _kernels as K
+    rows = T * k
+    y = (torch.arange(rows * H, device=DEV) % 23 - 11).to(torch.bfloat16).view(rows, H)
+    perm = torch.randperm(rows, device=DEV).to(torch.int32)
+    perm[::7] = -1
+    dscale = torch.randn(rows, device=DEV).to(torch.bfloat16)
+    gh, grw = K.combine_bwd(y, perm, T, k, dscale)
+    ref_h = K.combine(y, perm, T, k)
+    ref_rw = K.gather_route_grad(dscale, perm, (T, k))
+    torch.cuda.synchronize()
+    assert torch.equal(gh, ref_h) and torch.equal(grw, ref_rw)
+    p = perm.view(T, k).long()
+    want = torch.where(p >= 0, dscale.float()[p.clamp(min=0)], torch.zeros_like(grw))
+    assert torch.equal(grw, want)
