@@ -207,7 +207,13 @@ def main(argv=None):
            "| stage | kernels | kernel ms | bench stage ms | HBM read GB | HBM write GB | algorithmic GB | "
            "counter / algorithmic | algorithmic TB/s | TFLOP/s | clock GHz |",
            "|---|---|---|---|---|---|---|---|---|---|---|"] + rows + ["",
-           f"Sum of stage kernel times: {total:.3f} ms per step.", ""]
+           f"Sum of stage kernel times: {total:.3f} ms per step."]
+    side = [s for s in stages if bench["stages_ms"].get(s) is None and s != "route"]
+    if side:
+        md += ["", "Stages without a bench stage time ({}) ran on the backward's second stream beside the "
+               "next stage; their kernels overlap it, so the sum above exceeds the step time.".format(
+                   ", ".join(f"`{s}`" for s in side))]
+    md += [""]
     text = "\n".join(md)
     if a.md:
         open(a.md, "w").write(text)
