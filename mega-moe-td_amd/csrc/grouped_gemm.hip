@@ -682,10 +682,18 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
           else
             Mma::template frags<ATile, BTile, BK_>(fa[n], fb[n], nxt, nxt + ATile::ELEMS, wm, wn, 0, lane);
           mma.mfmas_t(fa[c], fb[c]);
-          if (ss == 0) ATile::put(nxt, ra);
+          // each operand's next loads go out as soon as its registers are in
+          // LDS: A (sub-step 0) one sub-step before B (sub-step 1), which
+          // gives A's gathered rows the longer latency cover (E32 step -1%,
+          // the Qwen-like dgrads -1 to -2%; issuing both at sub-step 0, with
+          // both LDS writes there, measured +3-6%)
+          if (ss == 0) {
+            ATile::put(nxt, ra);
+            la.load(ra, static_cast<int64_t>(min(kt + 2, nk - 1)) * BK_);
+          }
           if (ss == 1) {
             BTile::put(nxt + ATile::ELEMS, rb);
-            gload(min(kt + 2, nk - 1));
+            lb.load(rb, min(kt + 2, nk - 1) * b_step);
           }
 #pragma unroll
           for (int q = 0; q < Mma::MI * Mma::NI; ++q) {
