@@ -13,6 +13,7 @@ to it.
 
     python -m mega_moe.runtime.rocprof_summary --trace DIR --fetch DIR --write DIR \
         --clock DIR --cal-fetch DIR --cal-write DIR --bench JSON --md OUT.md --json OUT.json
+    python -m mega_moe.runtime.rocprof_summary --mfma DIR --bench JSON --title TITLE
 """
 
 from __future__ import annotations
@@ -136,12 +137,74 @@ def per_stage(disp_steps, steps: int, value):
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
+GEMM_LABELS = {"fc1_swiglu": "FC1 (gate/up + act)", "fc2": "FC2 (down)", "fc2_dgrad": "dAct = dY W2",
+               "fc2_wgrad": "dW2", "fc1_dgrad": "dX = dFC1 W1", "fc1_wgrad": "dW1"}
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
+
+
+def mfma_table(pmc_dir: str, bench: dict, title: str) -> str:
+    """MFMA utilisation of each GEMM stage's main kernel from one PMC pass of
+    SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE
+    (last step of the run): counted TFLOP = MOPS x 512, clock = GUI_ACTIVE /
+    8 XCDs / duration, MFMA busy = BUSY / (GUI_ACTIVE / 8 x 1024 SIMDs),
+    TFLOP/s = algorithmic flops (the bench line's) / duration."""
+    rows = _rows(pmc_dir, "*counter_collection.csv")
+    acc = {}
+    for r in rows:
+        d = acc.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"], "dur": int(r["End_Timestamp"]) -
+                                                    int(r["Start_Timestamp"]), "start": int(r["Start_Timestamp"])})
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    disp = sorted((k, v["name"], v["start"], v["start"] + v["dur"], v) for k, v in acc.items())
+    step = split_steps(disp)[-1]
+    out = [f"## {title}", "",
+           "| stage | kernel | us | algorithmic TFLOP | counted TFLOP | clock GHz | MFMA busy | TFLOP/s | "
+           "% of 2.5 PF | % of peak at clock |", "|---|---|---|---|---|---|---|---|---|---|"]
+    tot_fl = tot_us = 0.0
+    for stage, ds in assign_stages(step).items():
+        if stage not in GEMM_LABELS:
+            continue
+        main_k = [d for d in ds if "grouped_rows" in d[1] or "wgrad" in d[1]]
+        if not main_k:
+            continue
+        d = main_k[-1]
+        c = d[4]
+        us = c["dur"] / 1e3
+        g = bench["gemm_stages"][stage]
+        fl = g["TFLOP/s"] * 1e12 * g["ms"] * 1e-3
+        counted = c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0)
+        clock = gui / 8 / c["dur"]
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (gui / 8 * 1024) if gui else 0.0
+        tf = fl / (us * 1e-6) / 1e12
+        tot_fl += fl
+        tot_us += us
+        out.append(f"| {GEMM_LABELS[stage]} | `{short_name(d[1])}` | {us:.0f} | {fl / 1e12:.3f} | "
+                   f"{counted / 1e12:.3f} | {clock:.2f} | {busy * 100:.1f}% | {tf:.0f} | {tf / 2500 * 100:.1f}% | "
+                   f"{tf / (2500 * clock / 2.4) * 100:.1f}% |")
+    if tot_us:
+        tf = tot_fl / (tot_us * 1e-6) / 1e12
+        out += ["", f"All GEMMs of the step: {tot_fl / 1e12:.2f} TFLOP in {tot_us / 1e3:.2f} ms = {tf:.0f} TFLOP/s "
+                f"({tf / 2500 * 100:.1f}% of 2.5 PF)."]
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     for k in ("trace", "fetch", "write", "clock", "cal_fetch", "cal_write", "bench", "md", "json"):
         ap.add_argument("--" + k.replace("_", "-"), required=k not in ("md", "json", "clock"))
     ap.add_argument("--title", default="")
+    ap.add_argument("--mfma", help="PMC directory of the three MFMA counters: print the MFMA table instead")
     ap.add_argument("--commands", default="", help="text block of the commands that made the inputs")
+    if argv is None:
+        import sys
+        argv = sys.argv[1:]
+    if "--mfma" in argv:  # only --mfma, --bench and --title are needed
+        mp = argparse.ArgumentParser()
+        for k in ("mfma", "bench", "title"):
+            mp.add_argument("--" + k, required=k != "title", default="")
+        m, _ = mp.parse_known_args(argv)
+        print(mfma_table(m.mfma, json.load(open(m.bench)), m.title))
+        return
     a = ap.parse_args(argv)
 
     bench = json.load(open(a.bench))
