@@ -271,6 +271,18 @@ def main(argv=None):
            "counter / algorithmic | algorithmic TB/s | TFLOP/s | clock GHz |",
            "|---|---|---|---|---|---|---|---|---|---|---|"] + rows + ["",
            f"Sum of stage kernel times: {total:.3f} ms per step."]
+    stats = glob.glob(os.path.join(a.trace, "**", "*kernel_stats.csv"), recursive=True)
+    if stats:
+        # rocprofv3's own --stats summary of the same run (all launches of the
+        # run, warm-up and input generation included), the layer's kernels only
+        md += ["", "rocprofv3 `--stats` (kernel_stats.csv) of the traced run, the layer's kernels:", "",
+               "| kernel | calls | average us | total ms | % of GPU time |", "|---|---|---|---|---|"]
+        with open(stats[0], newline="") as f:
+            for r in csv.DictReader(f):
+                n = short_name(r["Name"])
+                if _is_layer_kernel(n):
+                    md.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                              f"{float(r['TotalDurationNs']) / 1e6:.2f} | {float(r['Percentage']):.2f} |")
     side = [s for s in stages if bench["stages_ms"].get(s) is None and s != "route"]
     if side:
         md += ["", "Stages without a bench stage time ({}) ran on the backward's second stream beside the "
