@@ -10,9 +10,12 @@
 // MI355X design
 //  * A workgroup of 8 wavefronts (2 per SIMD; 4 for the 128 x 128 tiles)
 //    computes a BM x BN tile with v_mfma_f32_32x32x16_bf16, each wave owning
-//    a (BM / WM) x (BN / WN) sub-tile.
-//  * Operands go global -> LDS with gfx950 LDS-DMA (global_load_lds_dwordx4)
-//    through an NST-stage ring, one barrier per K step. K-contiguous sources
+//    a (BM / WM) x (BN / WN) sub-tile. 256 x 256 tiles with K >= 1024 run 4
+//    wavefronts of 128 x 128 (one per SIMD, accumulators in the AGPRs) with
+//    register-staged operand copies interleaved with the MFMAs.
+//  * Otherwise operands go global -> LDS with gfx950 LDS-DMA
+//    (global_load_lds_dwordx4) through an NST-stage ring, one barrier per K
+//    step. K-contiguous sources
 //    sit in LDS as [rows][BK] with XOR-swizzled 16-byte slots and are read
 //    with ds_read_b128; M/N-contiguous sources (gate_up_weight [E, H, 2I],
 //    the natural down weight, both wgrad operands) keep their natural
