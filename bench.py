@@ -76,8 +76,8 @@ STAGE_KERNELS = {
     "fc2": "grouped_rows_kernel",
     "fc2_dgrad": "grouped_rows_kernel (gathered dy rows)",
     "fc1_dgrad": "grouped_rows_kernel (K-contiguous gate_up)",
-    "fc2_wgrad": "wgrad_persist_kernel / grouped_wgrad_kernel",
-    "fc1_wgrad": "wgrad_persist_kernel / grouped_wgrad_kernel",
+    "fc2_wgrad": "permute_kernel + wgrad_persist_kernel (small K) / grouped_wgrad_kernel (deep K)",
+    "fc1_wgrad": "permute_kernel + wgrad_persist_kernel (small K) / grouped_wgrad_kernel (deep K)",
 }
 
 # CPU-baseline sample per config: (tokens, experts). Where the layer's experts

@@ -211,9 +211,13 @@ def main(argv=None):
     steps = int(bench["steps"])
     trace_steps = split_steps(dispatches(a.trace))
     kernel_ms = per_stage(trace_steps, steps, lambda d: (d[3] - d[2]) * 1e-6)
+    # per kernel name within each stage: mean ms per step over the timed steps
     names = {}
-    for stage, ds in assign_stages(trace_steps[-1]).items():
-        names[stage] = sorted({short_name(d[1]) for d in ds})
+    for st in trace_steps[-steps:]:
+        for stage, ds in assign_stages(st).items():
+            per = names.setdefault(stage, {})
+            for d in ds:
+                per[short_name(d[1])] = per.get(short_name(d[1]), 0.0) + (d[3] - d[2]) * 1e-6 / steps
     fs, ws = calibration(a.cal_fetch, "FETCH_SIZE"), calibration(a.cal_write, "WRITE_SIZE")
     read_b = per_stage(split_steps(dispatches(a.fetch, "FETCH_SIZE")), 1, lambda d: d[4] * fs)
     write_b = per_stage(split_steps(dispatches(a.write, "WRITE_SIZE")), 1, lambda d: d[4] * ws)
@@ -251,7 +255,7 @@ def main(argv=None):
         def f(v, fmt):
             return "-" if v is None else format(v, fmt)
         rows.append("| {} | {} | {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
-            s, ", ".join(f"`{n}`" for n in names.get(s, [])), f(km, ".3f"), f(bm, ".3f"),
+            s, ", ".join(f"`{n}` {v:.3f}" for n, v in names.get(s, {}).items()), f(km, ".3f"), f(bm, ".3f"),
             f(None if rb is None else rb / 1e9, ".3f"), f(None if wb is None else wb / 1e9, ".3f"),
             f(None if ab is None else ab / 1e9, ".3f"),
             f(None if (ab is None or rb is None) else (rb + wb) / ab, ".2f"),
@@ -267,7 +271,7 @@ def main(argv=None):
            f"over the stage's launches of 100 us or more.", "",
            f"Bench line of the traced run: {bench['ms_per_step']:.3f} ms per step; roofline stage "
            f"`{bench['roofline'].get('stage')}` {bench['roofline']['kernel_ms']:.3f} ms (HIP events).", "",
-           "| stage | kernels | kernel ms | bench stage ms | HBM read GB | HBM write GB | algorithmic GB | "
+           "| stage | kernels (ms per step each) | kernel ms | bench stage ms | HBM read GB | HBM write GB | algorithmic GB | "
            "counter / algorithmic | algorithmic TB/s | TFLOP/s | clock GHz |",
            "|---|---|---|---|---|---|---|---|---|---|---|"] + rows + ["",
            f"Sum of stage kernel times: {total:.3f} ms per step."]
