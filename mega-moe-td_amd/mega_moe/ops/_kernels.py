@@ -23,12 +23,15 @@ class WorkspacePool:
     buffer stays valid for that graph's replays until ``release()``.
     ``FusedMoEForward`` owns one pool sized for its ``max_tokens_per_rank`` at
     the first forward, so its own calls never grow it; the module pool serves
-    direct calls of these wrappers.
+    direct calls of these wrappers and grows by powers of two
+    (``geometric``), so a caller with steadily growing sizes retires at most
+    one buffer per doubling per (device, stream, tag).
     """
 
-    def __init__(self):
+    def __init__(self, geometric: bool = False):
         self._live: dict = {}
         self._retired: list = []
+        self._geometric = geometric
 
     def get(self, device: torch.device, nbytes: int, tag: str) -> torch.Tensor:
         key = (str(device), torch.cuda.current_stream(device).cuda_stream, tag)
@@ -36,7 +39,10 @@ class WorkspacePool:
         if ws is None or ws.numel() < nbytes:
             if ws is not None:
                 self._retired.append(ws)
-            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            size = max(nbytes, 256)
+            if self._geometric:
+                size = 1 << (size - 1).bit_length()
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
             self._live[key] = ws
         return ws
 
@@ -49,7 +55,7 @@ class WorkspacePool:
         self._retired.clear()
 
 
-_POOL = WorkspacePool()
+_POOL = WorkspacePool(geometric=True)
 
 
 def workspace(device: torch.device, nbytes: int, tag: str, pool: WorkspacePool | None = None) -> torch.Tensor:

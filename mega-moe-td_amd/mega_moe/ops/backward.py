@@ -17,8 +17,9 @@ hand-written reference backward it is checked against
 Returned keys follow the reference: grad_hidden, grad_routing_weights,
 grad_fc1_1 / grad_fc1_2 ([E, F, H] views), grad_fc2 ([E, H, F]) and the
 intermediates grad_swiglu, grad_fc1_output, grad_gate, grad_fc1 (plus
-grad_fc2_out_sorted and grad_recv_hidden_sorted, derived when read); plus
-grad_gate_up, the packed [E, H, 2F] weight gradient.
+grad_fc2_out_sorted, derived when read, and grad_recv_hidden_sorted when
+``saved["_keep_grad_recv_hidden_sorted"]`` is set); plus grad_gate_up, the
+packed [E, H, 2F] weight gradient.
 """
 
 from __future__ import annotations
@@ -98,6 +99,7 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     stage_timing = os.environ.get("MOE_BWD_STAGE_TIMING") == "1"
     if stage_timing and tm is NULL_TIMER:
         tm = StageTimer()
+    tm.mark_pass()
     pool = saved.get("_workspaces")
     ws_rows = saved.get("_max_routes") or R
     # step 1: FC2 dgrad, B_e(k=h, n=f) = down[e, h, f]
@@ -161,9 +163,11 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
     tm.end()
 
     grads = _grad_dict(grad_hidden, grad_rw, grad_fc2, grad_gate_up, grad_act, dab, dscale, inter)
-    grads._bind(dy, send_token, offsets, dx)
+    # dx [R, H] is released here unless the caller asked to keep the
+    # pre-reduction FC1 input gradient (a per-stage check, not a training need)
+    grads._bind(dy, send_token, offsets, dx if saved.get("_keep_grad_recv_hidden_sorted") else None)
     if stage_timing:
-        _record_stage_sample(saved, tm)
+        _record_stage_sample(saved, tm, act_overlapped=side is not None)
     return grads
 
 
@@ -178,11 +182,15 @@ _BWD_INTERVALS = (
 )
 
 
-def _record_stage_sample(saved, timer):
+def _record_stage_sample(saved, timer, act_overlapped=False):
     """Append this pass's [dispatch, fc2_wgrad, swiglu, fc1_wgrad, combine]
-    milliseconds to saved["_bwd_stage_samples"] and print them (synchronises)."""
+    milliseconds to saved["_bwd_stage_samples"] and print them (synchronises).
+    With the activation backward on the second stream its time is inside
+    fc2_wgrad and the swiglu interval is NaN (not measured on its own)."""
     last = timer.last_pass()
     sample = [sum(last.get(s, 0.0) for s in stages) for _, stages in _BWD_INTERVALS]
+    if act_overlapped:
+        sample[[n for n, _ in _BWD_INTERVALS].index("swiglu")] = float("nan")
     saved.setdefault("_bwd_stage_samples", []).append(sample)
     print("[bwd-stage] " + " ".join(f"{v:8.3f}" for v in sample), flush=True)
 
@@ -196,8 +204,10 @@ class MoEGrads(dict):
     ``grad_fc2_out_sorted`` = dy gathered to the expert-major rows [M, H]
     (the backward's GEMMs read it in place, so it is materialised only when
     asked for) and ``grad_recv_hidden_sorted`` = the FC1 input gradient
-    [M, H] before the top-k reduce. M = number of valid routes (one host
-    read of the routing offsets).
+    [M, H] before the top-k reduce, kept only when the saved dict sets
+    ``_keep_grad_recv_hidden_sorted`` (it holds R x H bf16 otherwise freed
+    after the reduce). M = number of valid routes (one host read of the
+    routing offsets).
     """
 
     _DERIVED = ("grad_fc2_out_sorted", "grad_recv_hidden_sorted")
@@ -206,10 +216,9 @@ class MoEGrads(dict):
         self._src = (dy, send_token, offsets, dx)
 
     def __missing__(self, key):
-        src = getattr(self, "_src", None)
-        if key not in self._DERIVED or src is None:
+        if not self._has_derived(key):
             raise KeyError(key)
-        dy, send_token, offsets, dx = src
+        dy, send_token, offsets, dx = self._src
         m = int(offsets[-1].item())
         if key == "grad_fc2_out_sorted":
             value = K.permute(dy, send_token, offsets, m) if m else dy[:0].clone()
@@ -218,8 +227,14 @@ class MoEGrads(dict):
         self[key] = value
         return value
 
+    def _has_derived(self, key):
+        src = getattr(self, "_src", None)
+        if key not in self._DERIVED or src is None:
+            return False
+        return key != "grad_recv_hidden_sorted" or src[3] is not None
+
     def __contains__(self, key):
-        return dict.__contains__(self, key) or (key in self._DERIVED and getattr(self, "_src", None) is not None)
+        return dict.__contains__(self, key) or self._has_derived(key)
 
     def get(self, key, default=None):
         try:

@@ -424,7 +424,7 @@ class FusedMoEForward(torch.nn.Module):
             hidden_states=hidden_states, selected_experts=selected_experts, routing_weights=routing_weights,
             gate_up_weight=gate_up_weight, down_weight=down_weight, fc2=down_weight,
             _owner_token=id(self._routing_owner_token), _routing_generation=self._routing_generation,
-            _single_kernel_snapshot=False, _stage_timer=self.stage_timer,
+            _single_kernel_snapshot=bool(self.enable_single_kernel_forward), _stage_timer=self.stage_timer,
             _workspaces=self._workspaces, _max_routes=self.max_routes,
         )
         if tables is not None:

@@ -20,6 +20,7 @@ class StageTimer:
     def __init__(self):
         self._events = []          # list of (name, start_event, end_event)
         self._open = None
+        self._pass_start = 0       # index of the current pass's first event
 
     def begin(self, name: str):
         ev = torch.cuda.Event(enable_timing=True)
@@ -35,12 +36,19 @@ class StageTimer:
 
     def reset(self):
         self._events.clear()
+        self._pass_start = 0
+
+    def mark_pass(self):
+        """Start a new pass: ``last_pass`` reports only stages recorded after
+        this call."""
+        self._pass_start = len(self._events)
 
     def last_pass(self) -> dict:
-        """Milliseconds of each stage's most recent recording (synchronises)."""
+        """Milliseconds of each stage recorded since the last ``mark_pass``
+        (the latest recording of a name wins; synchronises)."""
         torch.cuda.synchronize()
         out = {}
-        for name, a, b in self._events:
+        for name, a, b in self._events[self._pass_start:]:
             out[name] = a.elapsed_time(b)
         return out
 
@@ -56,6 +64,9 @@ class StageTimer:
 
 class _NullTimer:
     def begin(self, name):
+        pass
+
+    def mark_pass(self):
         pass
 
     def end(self):

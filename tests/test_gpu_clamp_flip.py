@@ -1,0 +1,110 @@
+"""Clamped SwiGLU at the clamp limit (GPU): why a layer can fail the
+independent oracle's backward while every kernel is right.
+
+The clamped activation's derivative is a step function of the saved FC1
+value (kernels/swiglu_bwd.py:58-65: the gate's mask is ``g <= L``, the up
+projection's ``|u| <= L``). The build and the oracle both round FC1 to bf16
+(or to FP8 codes), but from fp32 sums taken in different orders, so a value
+one rounding step from L can land on either side of it. Then one element of
+``grad_fc1_output`` is zero on one side and the full derivative on the other,
+and that element carries into the FC1 weight gradient.
+
+Two layers of a 200-case fuzz failed the independent backward this way; each
+test below re-runs one with its fuzz seed and checks
+  (i)   the build's saved FC1 matches the oracle's within one rounding step
+        (bf16: one ulp; FP8: one code step, scales within one bf16 ulp),
+  (ii)  every element of ``grad_fc1_output`` that differs from the
+        oracle's own-forward backward by more than 2e-2 of its largest
+        magnitude sits where the two saves fall on opposite sides of the
+        limit (or in an FP8 group whose scale moved),
+  (iii) the oracle's backward on the build's own save agrees within the
+        2e-2 bar for every gradient, and per expert for the FC1 weight
+        gradient (the fuzz's failing check).
+"""
+
+import pytest
+import torch
+
+import mega_moe
+from mega_moe.bench_configs import CaseSpec, make_inputs
+from oracle import moe_oracle as O
+from tests._fc1_save import check_saved_fc1
+from tests._numeric import assert_rel, max_rel
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 0.05
+
+# (fuzz case, T, H, I, E, k, routing, saved FC1 format); inputs drawn with
+# make_inputs(seed=100 + case) as the fuzz did
+FLIP_CASES = [
+    (15, 4096, 1024, 1536, 32, 8, "zipf", "fp8"),
+    (132, 4096, 2048, 1024, 32, 8, "uniform_distinct", "bf16"),
+]
+
+
+def limit_flips(gu_gpu, gu_ref, inter):
+    """Elements whose clamp mask differs between the two saves: the gate
+    columns by ``g <= L``, the up columns by ``|u| <= L``."""
+    g1, g2 = gu_gpu[:, :inter], gu_ref[:, :inter]
+    u1, u2 = gu_gpu[:, inter:], gu_ref[:, inter:]
+    return torch.cat([(g1 <= LIMIT) != (g2 <= LIMIT), (u1.abs() <= LIMIT) != (u2.abs() <= LIMIT)], dim=1)
+
+
+@pytest.mark.parametrize("case", FLIP_CASES, ids=lambda c: f"fuzz{c[0]}-T{c[1]}-H{c[2]}-I{c[3]}-E{c[4]}-{c[7]}")
+def test_clamp_limit_flips_explain_mismatch(case):
+    i, T, H, I, E, k, routing, fmt = case
+    print(f"clamp flip case {case}", flush=True)
+    spec = CaseSpec("fuzz", T, H, I, E, k, routing, True)
+    inp = make_inputs(spec, device="cuda", seed=100 + i)
+    cfg = mega_moe.MoEForwardConfig(activation="clamp_swiglu", clamp_limit=LIMIT, save_fc1_dtype=fmt)
+    op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=T, hidden_size=H, top_k=k, num_experts=E, config=cfg)
+    x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
+    out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
+    g = mega_moe.moe_backward_triton(saved, dy, peer_mem=None)
+    torch.cuda.synchronize()
+    _, st = O.forward(x.cpu(), sel.cpu(), w1.cpu(), w2.cpu(), rw.cpu(), activation="clamp_swiglu",
+                      clamp_limit=LIMIT, save_fc1_dtype=fmt)
+    m = int(st["tables"]["offsets"][-1])
+    moved = check_saved_fc1(saved, st, m, fmt)                                        # (i)
+
+    ref_own = O.backward(st, dy.cpu())
+    dab_gpu = g["grad_fc1_output"][:m].float().cpu()
+    dab_own = ref_own["grad_fc1_output"].float()
+    gu_gpu = O.dequantize_fc1(saved["fc1_output"][:m].cpu(),
+                              None if fmt != "fp8" else saved["fc1_output_scale"][:m].cpu())
+    gu_ref = O.dequantize_fc1(st["fc1_output"], st.get("fc1_output_scale"))
+    explained = limit_flips(gu_gpu, gu_ref, I)
+    if moved is not None:
+        grp = O.FC1_SCALE_GROUP
+        explained |= moved.repeat_interleave(grp, dim=1)
+    # (ii) "off" is the 2e-2 bar of max |a - b| / max |b|, per element
+    off = (dab_gpu - dab_own).abs() > 2e-2 * float(dab_own.abs().max())
+    unexplained = off & ~explained
+    print(f"  flips {int(limit_flips(gu_gpu, gu_ref, I).sum())}, mismatching elements {int(off.sum())}, "
+          f"unexplained {int(unexplained.sum())}", flush=True)
+    assert not unexplained.any(), f"{int(unexplained.sum())} grad_fc1_output mismatches are not limit flips"
+    # away from the flips, the two backwards agree to the bar
+    assert_rel(dab_gpu[~explained], dab_own[~explained], 2e-2, "grad_fc1_output off the flips")
+
+    st["fc1_output"] = saved["fc1_output"][:m].cpu()                                  # (iii)
+    if fmt == "fp8":
+        st["fc1_output_scale"] = saved["fc1_output_scale"][:m].cpu()
+    st["act"] = saved["swiglu_out_weighted"][:m].float().cpu()
+    ref_gpu = O.backward(st, dy.cpu())
+    for name in ("grad_hidden", "grad_routing_weights", "grad_fc2", "grad_gate_up", "grad_fc1_output"):
+        assert_rel(g[name][:m] if name == "grad_fc1_output" else g[name], ref_gpu[name], 2e-2, name)
+    # per expert (the fuzz's check): a flipped element of grad_fc1_output
+    # moves a whole column of that expert's FC1 weight gradient, which can
+    # exceed 2e-2 of that expert's largest entry against the own-forward
+    # backward, but not against the backward on the build's save
+    worst_own = worst_gpu = 0.0
+    for e in range(E):
+        a, b = int(st["tables"]["offsets"][e]), int(st["tables"]["offsets"][e + 1])
+        if a == b:
+            continue
+        worst_own = max(worst_own, max_rel(g["grad_gate_up"][e], ref_own["grad_gate_up"][e]))
+        worst_gpu = max(worst_gpu, max_rel(g["grad_gate_up"][e], ref_gpu["grad_gate_up"][e]))
+    print(f"  per-expert grad_gate_up max-rel: own-forward {worst_own:.3e}, build's save {worst_gpu:.3e}",
+          flush=True)
+    assert worst_gpu <= 2e-2

@@ -41,6 +41,7 @@ def test_forward_backward_parity(spec, activation):
     cfg = {k: v for k, v in kw.items() if k != "activation"}
     op = _op(spec, activation, **cfg)
     out, saved = op.forward(inp["x"], sel, inp["gate_up"], inp["down"], inp["rw"], return_saved=True)
+    saved["_keep_grad_recv_hidden_sorted"] = True
     g = mega_moe.moe_backward_triton(saved, inp["dy"], peer_mem=None)
     torch.cuda.synchronize()
     ref_out, st = O.forward(inp["x"].cpu(), sel.cpu(), inp["gate_up"].cpu(), inp["down"].cpu(),
@@ -112,6 +113,37 @@ def test_autograd_function_matches_backward(fmt):
     with pytest.raises(RuntimeError, match="superseded"):
         out2.sum().backward()
     del out3
+
+
+def test_single_kernel_snapshot_shared_operator():
+    """enable_single_kernel_forward: one operator shared by two same-shape
+    layers runs forward A, forward B, backward B, backward A (the reference's
+    snapshot gate, ops/function.py:143-158 with _single_saved_adapter.py:369);
+    the default mode keeps rejecting the superseded backward."""
+    spec = SMALL[0]
+    op = _op(spec, enable_single_kernel_forward=True)
+    layers = []
+    for seed in (21, 22):
+        inp = make_inputs(spec, device="cuda", seed=seed, weight_scale=0.1)
+        x = inp["x"].clone().requires_grad_(True)
+        rw = inp["rw"].clone().requires_grad_(True)
+        w1 = inp["gate_up"].clone().requires_grad_(True)
+        w2 = inp["down"].contiguous().clone().requires_grad_(True)
+        out = mega_moe.MegaMoEFunction.apply(op, x, rw, inp["selected"], w1, w2, torch.empty(1, device="cuda"),
+                                             None)
+        layers.append((inp, x, rw, w1, w2, out))
+    for inp, x, rw, w1, w2, out in reversed(layers):
+        out.backward(inp["dy"])
+    torch.cuda.synchronize()
+    for inp, x, rw, w1, w2, out in layers:
+        ref_out, st = O.forward(inp["x"].cpu(), inp["selected"].cpu(), inp["gate_up"].cpu(),
+                                w2.detach().cpu(), inp["rw"].cpu())
+        ref = O.backward(st, inp["dy"].cpu())
+        assert_rel(out.detach(), ref_out, 2e-2, "out")
+        assert_rel(x.grad, ref["grad_hidden"], 2e-2, "dx")
+        assert_rel(rw.grad, ref["grad_routing_weights"], 2e-2, "drw")
+        assert_rel(w1.grad, ref["grad_gate_up"], 2e-2, "dw1")
+        assert_rel(w2.grad, ref["grad_fc2"], 2e-2, "dw2")
 
 
 def _sample_tokens(ref, spec, experts, n):
