@@ -171,14 +171,12 @@ int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_rows,
  *   c[e, n1, n2] = sum_{i in rows(e)} p[prow(i), n1] * q[qrow(i), n2]
  * prow(i) = p_rows[i] if p_rows != NULL else i (same for q). Output bf16
  * [E, N1, N2] contiguous; experts with no rows get zeros. max_rows is the
- * row capacity (an upper bound of offsets[E]); it selects the tiling. When
- * experts average <= 192 rows the output write dominates and a streaming
- * kernel runs over contiguous operands: gathered ones (p_rows / q_rows) are
- * first permuted into the workspace, which needs
- * mm_wgrad_workspace_bytes(max_rows, E, n1, n2) bytes (a smaller or NULL
- * workspace selects a slower kernel that gathers in place). That size
- * covers every call with at most max_rows rows, so a workspace sized for a
- * capacity serves all smaller calls.
+ * row capacity (an upper bound of offsets[E]); it selects the tiling (a
+ * persistent kernel bound by the output write when experts average <= 192
+ * rows, 256 x 256 tiles over the ragged K otherwise). Every kernel reads
+ * gathered rows (p_rows / q_rows) in place: the workspace arguments are
+ * unused and mm_wgrad_workspace_bytes returns 0 (both kept for ABI
+ * compatibility).
  * Replaces kernels/transposed_grouped_gemm.py:24-100 and the default
  * torch_npu grouped wgrad of ops/backward.py:85-94.
  */

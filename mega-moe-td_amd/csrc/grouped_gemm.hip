@@ -149,6 +149,14 @@ __device__ __forceinline__ void wait_stages(int n) {
   wait_vmcnt<0>();
 }
 
+// Two consecutive int32 at a wave-uniform address, loaded through the scalar
+// cache (completion tracked by lgkmcnt, not vmcnt).
+__device__ __forceinline__ int2 scalar_load_i32x2(const int32_t* p) {
+  uint64_t v;
+  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return make_int2(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(v >> 32));
+}
+
 // gfx950 transposing LDS read: within each 16-lane group, lane i receives
 // element (i % 4) of the 8-byte chunk read by lane 4*j + i/4, for j = 0..3.
 __device__ __forceinline__ v4i16 lds_read_tr16(const bf16* p) {
@@ -412,6 +420,7 @@ struct RowsArgs {
   int64_t ldc;
   const TileList* tl;
   int group_m;  // M tiles per grouped sweep of the N tiles
+  int krot;     // K-phase multiplier per N tile (K-contiguous B, LDS-DMA path); 0 = off
   // gated (FC1) epilogue
   const float* w;
   void* fc1_out;   // saved raw gate | up in fc1_fmt (MM_FC1_*), or null
@@ -616,15 +625,22 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
     lb.init_strided(bexp, p.b_sk, bcol);
     b_step = static_cast<int64_t>(BK_) * p.b_sk;
   }
+  const int nk = p.k / BK_;
+  // K-contiguous B (the dgrads' weights): each tile walks its K steps from
+  // its own phase, so that concurrently running tiles read different
+  // column ranges of their weight rows instead of the same offset of every
+  // row at once (the order of the fp32 sums changes with it)
+  const int kphase = (BLAYOUT == B_KCONTIG && p.krot > 0) ? (nt * p.krot) % nk : 0;
   auto issue = [&](int s) {
     bf16* buf = smem + (s % NST) * STAGE;
-    la.issue(buf, static_cast<int64_t>(s) * BK_);
-    lb.issue(buf + ATile::ELEMS, s * b_step);
+    int ks = s + kphase;
+    ks -= ks >= nk ? nk : 0;
+    la.issue(buf, static_cast<int64_t>(ks) * BK_);
+    lb.issue(buf + ATile::ELEMS, ks * b_step);
   };
 
   Mma mma;
   mma.zero();
-  const int nk = p.k / BK_;
   // waves whose row slab lies entirely past the tile's valid rows (the
   // partial last tile of an expert) skip their MFMAs; their accumulators stay
   // zero and those rows are never stored
@@ -877,21 +893,187 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
   }
 }
 
+
 __device__ __attribute__((aligned(256))) bf16 g_wgrad_zero_row[256];  // never written: all zeros
+
+// Deep-K weight gradient, register-staged (experts averaging more than
+// kRegWgradRows rows): 4 waves of 128 x 128 (one per SIMD, accumulators in
+// the AGPRs) over 256 x 256 output tiles, 64-row K steps, with the tile
+// schedule of grouped_wgrad_kernel. Each stage's 16-byte vectors are loaded
+// into VGPRs two stages ahead and written to a 2-deep LDS ring during the
+// MFMAs of the stage before, as in the row GEMM's register-staged loop; all
+// copies are ordinary loads, so the compiler's own wait counts cover them.
+// Wave w copies the stage's K rows 16w .. 16w + 15 (two per 1 KiB chunk);
+// the row ids of a gathered operand arrive one stage earlier, one load per
+// wave (lanes 0..15), and are broadcast with readlane. P rows past the
+// expert's end are read from a zero row (their products vanish), Q rows
+// there from a clamped real row, so the loop body has no branch. The
+// epilogue stages the tile in the (then idle) ring, XOR-swizzled, and stores
+// 2 rows x 512 B per instruction.
+template <int NT = 256>
+__global__ __launch_bounds__(NT) void wgrad_reg_kernel(WgradArgs a, int num_experts, int per_xcd) {
+  constexpr int BM = 256, BN = 256, BK_ = 64, WN = 2, WM = NT / 64 / WN;
+  using Mma = MmaTile<BM, BN, WM, WN>;
+  using PTile = MnTile<BM, BK_, NT>;
+  using QTile = MnTile<BN, BK_, NT>;
+  static_assert(NT == 256 && Mma::TM == 128 && Mma::TN == 128, "4 waves of 128 x 128");
+  constexpr int STAGE = PTile::ELEMS + QTile::ELEMS;
+  constexpr int PW = PTile::PER_WAVE;  // 1 KiB chunks per wave per operand per stage (8)
+  constexpr int KPC = PTile::KPC;      // K rows per chunk (2)
+  constexpr int RPW = PW * KPC;        // K rows per wave per stage (16)
+  static_assert(PW == QTile::PER_WAVE && KPC == QTile::KPC && RPW * (NT / 64) == BK_, "copy split");
+  __shared__ __attribute__((aligned(1024))) bf16 smem[2 * STAGE];
+  static_assert(BM * BN <= 2 * STAGE, "epilogue staging fits the ring");
+
+  const int t1n = a.n1 / BM, t2n = a.n2 / BN;
+  const int per_e = t1n * t2n;
+  const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int e = j / per_xcd;
+  const int t = x * per_xcd + (j - e * per_xcd);
+  if (e >= num_experts || t >= per_e) return;
+  int t1, t2;
+  grouped_mn(t, t1n, t2n, t1, t2);
+  const int r0 = min(a.offsets[e], a.rows_cap), r1 = min(a.offsets[e + 1], a.rows_cap);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int64_t pc = static_cast<int64_t>(t1) * BM, qc = static_cast<int64_t>(t2) * BN;
+  const int nk = (r1 - r0 + BK_ - 1) / BK_;
+  const int cap1 = a.rows_cap > 0 ? a.rows_cap - 1 : 0;
+  const int half = lane >> 5;   // which row of its chunk the lane copies
+  const int lcol = lane & 31;   // 16-byte slot of that row
+
+  // row ids of this wave's RPW rows of stage s (lane l holds row l % RPW);
+  // without a gather the load reads offsets[0] and its value is unused
+  auto load_ids = [&](const int32_t* rows, int s) -> int {
+    const int r = min(r0 + s * BK_ + wave * RPW + (lane & (RPW - 1)), cap1);
+    return *(rows ? rows + r : a.offsets);
+  };
+  auto src = [&](const bf16* base, int64_t ld, const int32_t* rows, int ids, int s, int v, int64_t col0,
+                 bool zero_tail) {
+    const int kl = wave * RPW + v * KPC + half;  // K row within the stage
+    const int kg = r0 + s * BK_ + kl;            // row of the expert-major order
+    const int lo = __builtin_amdgcn_readlane(ids, v * KPC), hi = __builtin_amdgcn_readlane(ids, v * KPC + 1);
+    const int row = rows ? (half ? hi : lo) : min(kg, cap1);
+    const int c = (lcol ^ mn_swz(kl)) * 8;
+    const uint64_t data = reinterpret_cast<uint64_t>(base + static_cast<int64_t>(row) * ld + col0 + c);
+    const uint64_t zero = reinterpret_cast<uint64_t>(g_wgrad_zero_row + c);
+    const uint64_t addr = (zero_tail && kg >= r1) ? zero : data;
+    return *reinterpret_cast<const u32x4_t*>(addr);
+  };
+  u32x4_t ra[PW], rb[PW];
+  int pid_cur = 0, qid_cur = 0, pid_nxt = 0, qid_nxt = 0;
+  auto gload_p = [&](int s) {
+#pragma unroll
+    for (int v = 0; v < PW; ++v) ra[v] = src(a.p, a.ldp, a.p_rows, pid_cur, s, v, pc, true);
+  };
+  auto gload_q = [&](int s) {
+#pragma unroll
+    for (int v = 0; v < PW; ++v) rb[v] = src(a.q, a.ldq, a.q_rows, qid_cur, s, v, qc, false);
+  };
+  // chunk v of wave w sits at LDS chunk w * PW + v (rows 2 (w PW + v) + 0/1)
+  auto put = [&](bf16* buf, const u32x4_t (&r)[PW]) {
+#pragma unroll
+    for (int v = 0; v < PW; ++v) *reinterpret_cast<u32x4_t*>(buf + (wave * PW + v) * kChunkElems + lane * 8) = r[v];
+  };
+
+  Mma mma;
+  mma.zero();
+  using Frag = bf16x8;
+  Frag fa[2][Mma::MI], fb[2][Mma::NI];
+  if (nk > 0) {
+    pid_cur = load_ids(a.p_rows, 0);
+    qid_cur = load_ids(a.q_rows, 0);
+    gload_p(0);
+    gload_q(0);
+    put(smem, ra);
+    put(smem + PTile::ELEMS, rb);
+    if (nk > 1) {
+      pid_cur = load_ids(a.p_rows, 1);
+      qid_cur = load_ids(a.q_rows, 1);
+      gload_p(1);
+      gload_q(1);
+      if (nk > 2) {
+        pid_nxt = load_ids(a.p_rows, 2);
+        qid_nxt = load_ids(a.q_rows, 2);
+      }
+    }
+  }
+  __syncthreads();
+  if (nk > 0) {
+    Mma::template frags<PTile, QTile, BK_>(fa[0], fb[0], smem, smem + PTile::ELEMS, wm, wn, 0, lane);
+    // sub-step ss issues its MFMAs from fragment set ss & 1 while the next
+    // sub-step's fragments load; stage kt + 1's registers go to LDS during
+    // sub-steps 0 (P) and 1 (Q), then stage kt + 2's loads issue (its row
+    // ids were loaded one stage before; stage kt + 3's go out with them);
+    // the barrier after sub-step 2 publishes stage kt + 1. Past the last
+    // stage the loads repeat it and the writes land in a slot nobody reads.
+    for (int kt = 0; kt < nk; ++kt) {
+      const bf16* cur = smem + (kt & 1) * STAGE;
+      bf16* nxt = smem + ((kt + 1) & 1) * STAGE;
+      const int s2 = min(kt + 2, nk - 1);
+#pragma unroll
+      for (int ss = 0; ss < 4; ++ss) {
+        const int c = ss & 1, n = c ^ 1;
+        if (ss < 3)
+          Mma::template frags<PTile, QTile, BK_>(fa[n], fb[n], cur, cur + PTile::ELEMS, wm, wn, (ss + 1) * 16, lane);
+        else
+          Mma::template frags<PTile, QTile, BK_>(fa[n], fb[n], nxt, nxt + PTile::ELEMS, wm, wn, 0, lane);
+        mma.mfmas_t(fa[c], fb[c]);
+        if (ss == 0) {
+          put(nxt, ra);
+          pid_cur = pid_nxt;
+          qid_cur = qid_nxt;
+          gload_p(s2);
+        }
+        if (ss == 1) {
+          put(nxt + PTile::ELEMS, rb);
+          gload_q(s2);
+          pid_nxt = load_ids(a.p_rows, min(kt + 3, nk - 1));
+          qid_nxt = load_ids(a.q_rows, min(kt + 3, nk - 1));
+        }
+#pragma unroll
+        for (int q = 0; q < Mma::MI * Mma::NI; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+        if (ss == 2) __syncthreads();
+      }
+    }
+  }
+  __syncthreads();
+  // epilogue: transposed accumulators (lane: row lane % 32 of block i, 4
+  // consecutive columns); 16-byte slot v of tile row r at v ^ (r & 31)
+  constexpr int VPR = BN / 8;
+#pragma unroll
+  for (int i = 0; i < Mma::MI; ++i)
+#pragma unroll
+    for (int jj = 0; jj < Mma::NI; ++jj)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int tr = wm * Mma::TM + i * 32 + (lane & 31);
+        const int tc = wn * Mma::TN + jj * 32 + Mma::acc_col(g, lane);
+        *reinterpret_cast<uint2*>(smem + tr * BN + ((((tc >> 3) ^ (tr & 31)) << 3) | (tc & 7))) =
+            make_uint2(pack_bf16x2(mma.acc[i][jj][4 * g], mma.acc[i][jj][4 * g + 1]),
+                       pack_bf16x2(mma.acc[i][jj][4 * g + 2], mma.acc[i][jj][4 * g + 3]));
+      }
+  __syncthreads();
+  bf16* out = a.c + static_cast<int64_t>(e) * a.n1 * a.n2 + pc * a.n2 + qc;
+#pragma unroll 4
+  for (int idx = threadIdx.x; idx < BM * VPR; idx += NT) {
+    const int r = idx / VPR, cv = idx % VPR;
+    store_out16(out + static_cast<int64_t>(r) * a.n2 + cv * 8,
+                *reinterpret_cast<const uint4*>(smem + r * BN + ((cv ^ (r & 31)) << 3)));
+  }
+}
 
 // ------------------------------------------------------------------ small-K wgrad
 //
 // Weight gradient when experts hold few rows (K of the GEMM; e.g. 73 rows
 // per expert at 4096 tokens, top-16 over 896 experts): the E x n1 x n2 bf16
 // output write dominates.
-
-// Two consecutive int32 at a wave-uniform address, loaded through the scalar
-// cache (completion tracked by lgkmcnt, not vmcnt).
-__device__ __forceinline__ int2 scalar_load_i32x2(const int32_t* p) {
-  uint64_t v;
-  asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-  return make_int2(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(v >> 32));
-}
 
 // wait until at most n (rounded down to a multiple of STEP) vector-memory
 // ops of this wave are outstanding; n is wave-uniform
@@ -908,8 +1090,8 @@ __device__ __forceinline__ void wait_vmcnt_atmost(int n) {
   }
 }
 
-// Small-K weight gradient over contiguous operands (gathered operands are
-// permuted into the workspace first by the host side).
+// Small-K weight gradient; gathered operands are read in place (the row ids
+// of each stage come from scalar loads).
 //  * Persistent: one 8-wave workgroup per CU walks a sequence of (expert,
 //    256 x 256 output tile, 32-row K step) stages through an NST-deep LDS
 //    ring, so the first stages of the next tile are in flight while the
@@ -1014,21 +1196,53 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
   TileCursor cc, lc;  // consumer; copier (NST - 1 stages ahead)
   cc.init(x, kXcds * teams, c, per_e, num_experts, a.offsets, a.rows_cap);
   lc = cc;
+  // Gathered operands: instruction v of this wave copies the stage's K rows
+  // k0(v) .. k0(v) + KPC - 1 (k0 wave-uniform), so their row ids come from
+  // scalar loads and each lane picks its own. The ids of a stage are loaded
+  // as soon as the copier's cursor reaches it, one stage before its copies
+  // are issued, so the loads are in flight meanwhile. Rows past the
+  // expert's end are read from a zero row.
+  constexpr int KPC = PTile::KPC;
+  static_assert(PTile::KPC == QTile::KPC && PTile::PER_WAVE == QTile::PER_WAVE, "one K-row split for both operands");
+  constexpr int PW = PTile::PER_WAVE;
+  const int cap1 = a.rows_cap > 0 ? a.rows_cap - 1 : 0;
+  int pid[PW][KPC], qid[PW][KPC];
+  auto load_ids = [&](const TileCursor& q) {
+    const int rbase = q.r0 + q.ks * BKS;
+#pragma unroll
+    for (int v = 0; v < PW; ++v)
+#pragma unroll
+      for (int j = 0; j < KPC; ++j) {
+        const int r = min(rbase + (v * (NT / 64) + wave) * KPC + j, cap1);
+        pid[v][j] = a.p_rows ? *(const const_i32*)(a.p_rows + r) : 0;
+        qid[v][j] = a.q_rows ? *(const const_i32*)(a.q_rows + r) : 0;
+      }
+  };
+  auto row_src = [&](const bf16* base, int64_t ld, bool gathered, const int (&id)[KPC], int rbase, int kv, int k0,
+                     int k, int64_t col) -> const bf16* {
+    int64_t r = rbase + k;
+    if (gathered) {
+      int pick = id[0];
+#pragma unroll
+      for (int j = 1; j < KPC; ++j) pick = (k - k0 == j) ? id[j] : pick;
+      r = pick;
+    }
+    return k < kv ? base + r * ld + col : g_wgrad_zero_row;
+  };
   auto issue = [&](const TileCursor& q, int buf) {
     bf16* dst = smem + buf * STAGE;
     int t1, t2;
     tile_of(q.t, t1, t2);
     const int kb = q.ks * BKS;
-    const bf16* prow0 = a.p + static_cast<int64_t>(q.r0 + kb) * a.ldp + t1 * BM;
-    const bf16* qrow0 = a.q + static_cast<int64_t>(q.r0 + kb) * a.ldq + t2 * BN;
+    const int rbase = q.r0 + kb;
     const int kv = q.kr - kb;
     PTile::issue_rows(dst, [&](int v) {
-      const int k = PTile::k_of(v);
-      return k < kv ? prow0 + static_cast<int64_t>(k) * a.ldp : g_wgrad_zero_row;
+      return row_src(a.p, a.ldp, a.p_rows != nullptr, pid[v], rbase, kv, (v * (NT / 64) + wave) * KPC,
+                     PTile::k_of(v), static_cast<int64_t>(t1) * BM);
     });
     QTile::issue_rows(dst + PTile::ELEMS, [&](int v) {
-      const int k = QTile::k_of(v);
-      return k < kv ? qrow0 + static_cast<int64_t>(k) * a.ldq : g_wgrad_zero_row;
+      return row_src(a.q, a.ldq, a.q_rows != nullptr, qid[v], rbase, kv, (v * (NT / 64) + wave) * KPC,
+                     QTile::k_of(v), static_cast<int64_t>(t2) * BN);
     });
   };
 
@@ -1039,6 +1253,7 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
 #pragma unroll
   for (int i = 0; i < NST; ++i) stage_mark[i] = 0;
   int nissued = 0;
+  if (lc.valid) load_ids(lc);
   for (; nissued < NST - 1 && lc.valid; ++nissued) {
     issue(lc, nissued % NST);
     issued_ops += LPS;
@@ -1046,6 +1261,7 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
     for (int i = 0; i < NST; ++i)
       if (i == nissued % NST) stage_mark[i] = issued_ops;
     lc.advance(c, nc, per_e, num_experts, a.offsets, a.rows_cap);
+    if (lc.valid) load_ids(lc);
   }
   Mma mma;
   mma.zero();
@@ -1063,6 +1279,7 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
       for (int i = 0; i < NST; ++i)
         if (i == nissued % NST) stage_mark[i] = issued_ops;
       lc.advance(c, nc, per_e, num_experts, a.offsets, a.rows_cap);
+      if (lc.valid) load_ids(lc);
       ++nissued;
     }
     const bf16* pb = smem + (st % NST) * STAGE;
@@ -1209,6 +1426,21 @@ int device_cus() {
 // (Kimi-scale 8192 tokens, 146 rows: FC1 wgrad 16.3 -> 15.7 ms against the
 // deep-K kernel; 16384 tokens, 292 rows: deep-K 22.9 against 24.7 ms).
 constexpr int64_t kSmallKRows = 192;
+
+// Deep-K 256 x 256 weight gradient: the register-staged 4-wave kernel when
+// experts average more than kRegWgradRows rows (Skew-like layer, 4096 rows
+// per expert: dW1 3.47 -> 3.31 ms, dW2 1.99 -> 1.92 ms against 8 waves with
+// LDS-DMA copies); below that the 8-wave kernel's second wave per SIMD
+// hides the per-tile prologue and epilogue better (Qwen-like, 512 rows:
+// dW1 0.585 against 0.62 ms). MM_WGRAD_REG=0 / 1 forces the choice.
+constexpr int64_t kRegWgradRows = 2048;
+bool wgrad_reg(int64_t max_rows, int E) {
+  if (const char* e = getenv("MM_WGRAD_REG")) {
+    if (strcmp(e, "0") == 0) return false;
+    if (strcmp(e, "1") == 0) return true;
+  }
+  return max_rows > kRegWgradRows * static_cast<int64_t>(E);
+}
 bool wgrad_small_k(int64_t max_rows, int E) { return max_rows <= kSmallKRows * static_cast<int64_t>(E); }
 
 template <int BLAYOUT, int EPI>
@@ -1221,6 +1453,7 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   // expert's N tiles run together, so its gathered A panel stays in L2
   // (Kimi-scale: -5% layer time against 8-deep groups)
   p.group_m = c.bm == 128 ? 1 : GROUP_M;
+  if (const char* ev = getenv("MM_KROT")) p.krot = atoi(ev);
   if (c.bm == 256) {
     if (rows_lds_dma() || p.k < 1024)
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
@@ -1336,13 +1569,13 @@ extern "C" int mm_grouped_gemm(const uint16_t* a, int64_t lda, const int32_t* a_
   return run_rows<B_NCONTIG, EPI_STORE>(p, offsets, max_rows, num_experts, workspace, s, "mm_grouped_gemm");
 }
 
-// Bytes that any call with at most max_rows rows needs: calls above the
-// small-K bound use the deep-K kernel and no workspace, so the largest need
-// is at min(max_rows, that bound).
+// Every weight-gradient kernel gathers its rows in place: no workspace.
 extern "C" size_t mm_wgrad_workspace_bytes(int64_t max_rows, int32_t num_experts, int32_t n1, int32_t n2) {
-  if (max_rows <= 0 || num_experts <= 0) return 0;
-  const int64_t r = std::min<int64_t>(max_rows, kSmallKRows * static_cast<int64_t>(num_experts));
-  return mm_align_up(static_cast<size_t>(r) * n1 * 2, 256) + static_cast<size_t>(r) * n2 * 2;
+  (void)max_rows;
+  (void)num_experts;
+  (void)n1;
+  (void)n2;
+  return 0;
 }
 
 extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p_rows, const uint16_t* q,
@@ -1358,9 +1591,8 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
               q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c), static_cast<int>(max_rows)};
   hipStream_t s = mm_hip_stream(stream);
   // Experts averaging <= 192 rows (K of the wgrad GEMM): the output write
-  // dominates -> 256 x 256 tiles over contiguous operands when n1, n2 allow
-  // and the workspace can hold the permuted copies of gathered operands
-  // (WG_WIDE), else 128 x 128 tiles that gather in place (WG_TILE).
+  // dominates -> the persistent 256 x 256-tile kernel when n1, n2 allow
+  // (WG_WIDE), else 128 x 128 tiles (WG_TILE); both gather rows in place.
   // Otherwise 256-wide tiles with a deep K loop (WG_LARGE).
   // MM_WGRAD_KERNEL=wide|tile|large overrides the choice (wide falls back
   // to tile where it does not apply).
@@ -1371,25 +1603,10 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
     else if (strcmp(ev, "large") == 0) variant = WG_LARGE;
   }
   if (variant == WG_WIDE) {
-    const size_t pb = p_rows ? mm_align_up(static_cast<size_t>(max_rows) * n1 * 2, 256) : 0;
-    const size_t qb = q_rows ? static_cast<size_t>(max_rows) * n2 * 2 : 0;
-    if (n1 % 256 != 0 || n2 % 256 != 0 || (pb + qb > 0 && (!workspace || workspace_bytes < pb + qb))) {
+    if (n1 % 256 != 0 || n2 % 256 != 0) {
       variant = WG_TILE;
     } else {
-      uint16_t* wsp = static_cast<uint16_t*>(workspace);
-      if (p_rows) {
-        if (int rc = mm_permute(p, ldp, p_rows, offsets, num_experts, max_rows, n1, wsp, n1, stream)) return rc;
-        a.p = reinterpret_cast<const bf16*>(wsp);
-        a.ldp = n1;
-        a.p_rows = nullptr;
-      }
-      if (q_rows) {
-        uint16_t* qd = wsp + pb / 2;
-        if (int rc = mm_permute(q, ldq, q_rows, offsets, num_experts, max_rows, n2, qd, n2, stream)) return rc;
-        a.q = reinterpret_cast<const bf16*>(qd);
-        a.ldq = n2;
-        a.q_rows = nullptr;
-      }
+      if (max_rows == 0) a.p_rows = a.q_rows = nullptr;  // no row is read: every tile is zero
       const int g = device_cus() / kXcds * kXcds;
       wgrad_persist_kernel<kWideStages><<<g > 0 ? g : kXcds, 512, 0, s>>>(a, num_experts);
       return mm_check_launch("mm_grouped_wgrad");
@@ -1407,7 +1624,11 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   if (small) {
     grouped_wgrad_kernel<128, 128, 32, 2, true><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bm == 256 && bn == 256) {
-    grouped_wgrad_kernel<256, 256, 64, 2, false, 512><<<grid, 512, 0, s>>>(a, num_experts, px);
+    if (wgrad_reg(max_rows, num_experts)) {
+      wgrad_reg_kernel<><<<grid, 256, 0, s>>>(a, num_experts, px);
+    } else {
+      grouped_wgrad_kernel<256, 256, 64, 2, false, 512><<<grid, 512, 0, s>>>(a, num_experts, px);
+    }
   } else if (bm == 256) {
     grouped_wgrad_kernel<256, 128, 64, 2, false><<<grid, kThreads, 0, s>>>(a, num_experts, px);
   } else if (bn == 256) {

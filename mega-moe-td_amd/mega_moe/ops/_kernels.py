@@ -158,8 +158,9 @@ def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int
                   ws_rows: int | None = None) -> torch.Tensor:
     """c[e] = P_e^T Q_e over each expert's rows -> [E, n1, n2] bf16.
 
-    ``ws_rows`` (>= max_rows) sizes the workspace, so a pool sized once for an
-    operator's capacity is reused by smaller calls."""
+    Gathered rows (``p_rows`` / ``q_rows``) are read in place; the kernels
+    take no workspace (``pool`` and ``ws_rows`` are accepted for the callers
+    that pass them)."""
     _check_bf16("p", p)
     _check_bf16("q", q)
     if p.stride(1) != 1 or q.stride(1) != 1 or p.shape[1] != n1 or q.shape[1] != n2:
@@ -168,11 +169,9 @@ def grouped_wgrad(p, p_rows, q, q_rows, offsets, n1: int, n2: int, max_rows: int
     if max_rows is None:
         max_rows = q.shape[0] if q_rows is None else q_rows.shape[0]
     c = torch.empty(num_experts, n1, n2, dtype=torch.bfloat16, device=p.device)
-    need = wgrad_workspace_bytes(max(max_rows, ws_rows or 0), num_experts, n1, n2)
-    ws = workspace(p.device, need, "wgrad", pool) if need and (p_rows is not None or q_rows is not None) else None
     _lib.call("mm_grouped_wgrad", _lib.ptr(p), p.stride(0), _lib.ptr(p_rows), _lib.ptr(q), q.stride(0),
-              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), _lib.ptr(ws),
-              0 if ws is None else ws.numel(), _lib.stream_of(p.device))
+              _lib.ptr(q_rows), _lib.ptr(offsets), num_experts, max_rows, n1, n2, _lib.ptr(c), None, 0,
+              _lib.stream_of(p.device))
     return c
 
 

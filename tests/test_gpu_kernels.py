@@ -135,10 +135,12 @@ def test_grouped_gemm(layout, kind, gather):
 
 @pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
 @pytest.mark.parametrize("gather", [False, True])
-@pytest.mark.parametrize("tiling", ["wide", "tile", "large"])
+@pytest.mark.parametrize("tiling", ["wide", "tile", "large", "large_reg"])
 def test_grouped_wgrad(kind, gather, tiling, monkeypatch):
     from mega_moe.ops import _kernels as K
-    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling)  # the kernel variant; read on every call
+    # the kernel variant; read on every call ("large_reg": the register-staged deep-K kernel)
+    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling.split("_")[0])
+    monkeypatch.setenv("MM_WGRAD_REG", "1" if tiling == "large_reg" else "0")
     E, N1, N2 = 5, 256, 256
     offs = _ragged(E, kind, seed=4)
     M = int(offs[-1])
@@ -162,13 +164,14 @@ def test_grouped_wgrad(kind, gather, tiling, monkeypatch):
 
 
 @pytest.mark.parametrize("shape", [(512, 1280), (1280, 512)], ids=["n2_tiles_more", "n1_tiles_more"])
-@pytest.mark.parametrize("tiling", ["wide", "tile"])
+@pytest.mark.parametrize("tiling", ["wide", "tile", "large_reg"])
 def test_grouped_wgrad_many_experts_both_gathered(tiling, shape, monkeypatch):
     """Small-K regime with many experts: rows 0..140 per expert (zero-row
     experts, a last K stage of <= 16 rows, multi-stage K, one 300-row
-    expert), both operands gathered (permuted into the workspace first)."""
+    expert), both operands gathered (read in place)."""
     from mega_moe.ops import _kernels as K
-    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling)
+    monkeypatch.setenv("MM_WGRAD_KERNEL", tiling.split("_")[0])
+    monkeypatch.setenv("MM_WGRAD_REG", "1" if tiling == "large_reg" else "0")
     E = 21
     N1, N2 = shape  # both tile walks of the small-K kernel (more tiles along n1 or along n2)
     rng = np.random.default_rng(11)
