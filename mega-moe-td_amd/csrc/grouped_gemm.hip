@@ -125,10 +125,15 @@ constexpr int kChunkElems = 512;  // 1 KiB of bf16 per wave instruction
 // adds no conservative vmcnt(0) before later LDS reads (it would otherwise
 // serialise every prefetch); completion is awaited explicitly with
 // wait_vmcnt<N>() + a barrier. M0 (the LDS destination) is written only here.
+// POL 1: non-temporal (streamed once; kept from displacing reused lines).
+template <int POL = 0>
 __device__ __forceinline__ void copy16_to_lds(const bf16* src, bf16* lds_chunk) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(lds_chunk))));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
+  if constexpr (POL == 1)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0) : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory");
 }
 
 // s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
@@ -192,16 +197,24 @@ struct KcTile {
       ptr[v] = row_ptr(r) + ((q % VPR) ^ swz(r)) * 8;
     }
   }
+  template <int POL = 0>
   __device__ void issue(bf16* lds, int64_t k0) const {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + k0, lds + (v * (NT / 64) + wave) * kChunkElems);
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds<POL>(ptr[v] + k0, lds + (v * (NT / 64) + wave) * kChunkElems);
   }
   // Register-staged copy: the same vectors as issue(), loaded into VGPRs now
   // and written to the same LDS positions by put() later.
+  template <int POL = 0>
   __device__ void load(u32x4_t (&r)[PER_WAVE], int64_t k0) const {
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) r[v] = *reinterpret_cast<const u32x4_t*>(ptr[v] + k0);
+    for (int v = 0; v < PER_WAVE; ++v) {
+      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(ptr[v] + k0);
+      if constexpr (POL == 1)
+        r[v] = __builtin_nontemporal_load(q);
+      else
+        r[v] = *q;
+    }
   }
   __device__ static void put(bf16* lds, const u32x4_t (&r)[PER_WAVE]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -249,14 +262,22 @@ struct MnTile {
 #pragma unroll
     for (int v = 0; v < PER_WAVE; ++v) ptr[v] = base + static_cast<int64_t>(k_of(v)) * ld + col_off(col_of(v));
   }
+  template <int POL = 0>
   __device__ void issue(bf16* lds, int64_t off) const {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds(ptr[v] + off, lds + (v * (NT / 64) + wave) * kChunkElems);
+    for (int v = 0; v < PER_WAVE; ++v) copy16_to_lds<POL>(ptr[v] + off, lds + (v * (NT / 64) + wave) * kChunkElems);
   }
+  template <int POL = 0>
   __device__ void load(u32x4_t (&r)[PER_WAVE], int64_t off) const {
 #pragma unroll
-    for (int v = 0; v < PER_WAVE; ++v) r[v] = *reinterpret_cast<const u32x4_t*>(ptr[v] + off);
+    for (int v = 0; v < PER_WAVE; ++v) {
+      const u32x4_t* q = reinterpret_cast<const u32x4_t*>(ptr[v] + off);
+      if constexpr (POL == 1)
+        r[v] = __builtin_nontemporal_load(q);
+      else
+        r[v] = *q;
+    }
   }
   __device__ static void put(bf16* lds, const u32x4_t (&r)[PER_WAVE]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -420,7 +441,6 @@ struct RowsArgs {
   int64_t ldc;
   const TileList* tl;
   int group_m;  // M tiles per grouped sweep of the N tiles
-  int krot;     // K-phase multiplier per N tile (K-contiguous B, LDS-DMA path); 0 = off
   // gated (FC1) epilogue
   const float* w;
   void* fc1_out;   // saved raw gate | up in fc1_fmt (MM_FC1_*), or null
@@ -572,7 +592,8 @@ __device__ __forceinline__ void rows_epilogue(const RowsArgs& p, bf16* smem, con
 // REG: operands are loaded into VGPRs one stage ahead and written to a
 // 2-deep LDS ring with ordinary LDS stores after each stage's MFMAs (one
 // barrier per K step), instead of LDS-DMA copies.
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, int ACT = 0, bool REG = false>
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, int ACT = 0, bool REG = false,
+          int BPOL = 0>
 __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
   constexpr int WN = 2, WM = NT / 64 / WN;  // 4 waves: 2x2, 8 waves: 4x2
   using Mma = MmaTile<BM, BN, WM, WN>;
@@ -625,22 +646,15 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
     lb.init_strided(bexp, p.b_sk, bcol);
     b_step = static_cast<int64_t>(BK_) * p.b_sk;
   }
-  const int nk = p.k / BK_;
-  // K-contiguous B (the dgrads' weights): each tile walks its K steps from
-  // its own phase, so that concurrently running tiles read different
-  // column ranges of their weight rows instead of the same offset of every
-  // row at once (the order of the fp32 sums changes with it)
-  const int kphase = (BLAYOUT == B_KCONTIG && p.krot > 0) ? (nt * p.krot) % nk : 0;
   auto issue = [&](int s) {
     bf16* buf = smem + (s % NST) * STAGE;
-    int ks = s + kphase;
-    ks -= ks >= nk ? nk : 0;
-    la.issue(buf, static_cast<int64_t>(ks) * BK_);
-    lb.issue(buf + ATile::ELEMS, ks * b_step);
+    la.issue(buf, static_cast<int64_t>(s) * BK_);
+    lb.template issue<BPOL>(buf + ATile::ELEMS, s * b_step);
   };
 
   Mma mma;
   mma.zero();
+  const int nk = p.k / BK_;
   // waves whose row slab lies entirely past the tile's valid rows (the
   // partial last tile of an expert) skip their MFMAs; their accumulators stay
   // zero and those rows are never stored
@@ -662,7 +676,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
     u32x4_t ra[ATile::PER_WAVE], rb[BTile::PER_WAVE];
     auto gload = [&](int s) {
       la.load(ra, static_cast<int64_t>(s) * BK_);
-      lb.load(rb, s * b_step);
+      lb.template load<BPOL>(rb, s * b_step);
     };
     auto sput = [&](int s) {
       bf16* buf = smem + (s & 1) * STAGE;
@@ -712,7 +726,7 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
           }
           if (ss == 1) {
             BTile::put(nxt + ATile::ELEMS, rb);
-            lb.load(rb, min(kt + 2, nk - 1) * b_step);
+            lb.template load<BPOL>(rb, min(kt + 2, nk - 1) * b_step);
           }
 #pragma unroll
           for (int q = 0; q < Mma::MI * Mma::NI; ++q) {
@@ -1359,7 +1373,7 @@ RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
   return c;
 }
 
-template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, bool REG = false>
+template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, bool REG = false, int BPOL = 0>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
   const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
@@ -1371,7 +1385,7 @@ void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) 
     else
       grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, MM_ACT_SITUGLU, REG><<<grid, NT, 0, s>>>(p);
   } else {
-    grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, 0, REG><<<grid, NT, 0, s>>>(p);
+    grouped_rows_kernel<BM, BN, BK_, NST, BLAYOUT, EPI, NT, 0, REG, BPOL><<<grid, NT, 0, s>>>(p);
   }
 }
 
@@ -1402,6 +1416,13 @@ bool rows_lds_dma() {
     v = (e && strcmp(e, "1") == 0) ? 1 : 0;
   }
   return v == 1;
+}
+
+// Non-temporal weight copies in the 128-row row-GEMM tiles unless
+// MM_WEIGHT_NT=0 (read on every call).
+bool weight_nt() {
+  const char* e = getenv("MM_WEIGHT_NT");
+  return !(e && strcmp(e, "0") == 0);
 }
 
 enum { WG_WIDE = 0, WG_TILE = 1, WG_LARGE = 2 };
@@ -1453,7 +1474,6 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   // expert's N tiles run together, so its gathered A panel stays in L2
   // (Kimi-scale: -5% layer time against 8-deep groups)
   p.group_m = c.bm == 128 ? 1 : GROUP_M;
-  if (const char* ev = getenv("MM_KROT")) p.krot = atoi(ev);
   if (c.bm == 256) {
     if (rows_lds_dma() || p.k < 1024)
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
@@ -1466,16 +1486,32 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     // the K-contiguous dgrads, which keep 256). BK 32 x 4 stages (4 x 40 KiB)
     // keeps three stages of weight in flight per CU instead of one 80 KiB
     // stage (Kimi-scale FC1 -4%, FC2 -6% against BK 64 x 2).
+    // The weight tiles of these 128-row (weight-streaming) launches are read
+    // once, so their LDS-DMA copies carry the non-temporal hint and do not
+    // displace the activation panels that every N tile of an expert reuses
+    // from L2 (Kimi-scale FC2 4.69 -> 4.40 ms, FC2 dgrad 4.47 -> 4.13 ms,
+    // FC1 dgrad 9.52 -> 8.98 ms, FC1 unchanged; MM_WEIGHT_NT=0 drops it).
+    const bool wnt = weight_nt();
     bool wide = false;
     if constexpr (BLAYOUT == B_NCONTIG) {
       wide = p.n % 512 == 0;
-      if (wide) launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+      if (wide) {
+        if (wnt)
+          launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512, false, 1>(p, max_rows, E, s);
+        else
+          launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+      }
     }
     if (!wide) {
-      if (eight_waves())  // 32-row wave slabs: rows past a small expert's count skip more MFMAs
-        launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
-      else
+      // 8 waves: 32-row wave slabs, so rows past a small expert's count skip more MFMAs
+      if (eight_waves()) {
+        if (wnt)
+          launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512, false, 1>(p, max_rows, E, s);
+        else
+          launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI, 512>(p, max_rows, E, s);
+      } else {
         launch_rows_cfg<128, 256, 64, 3, BLAYOUT, EPI>(p, max_rows, E, s);
+      }
     }
   } else {
     launch_rows_cfg<128, 128, 64, 4, BLAYOUT, EPI>(p, max_rows, E, s);
