@@ -133,6 +133,71 @@ def test_grouped_gemm(layout, kind, gather):
     assert_rel(c[:M], ref, 1e-2, "grouped_gemm")
 
 
+@pytest.mark.parametrize("layout", ["kcontig", "ncontig"])
+@pytest.mark.parametrize("gather", [False, True])
+def test_grouped_gemm_ragged_tails(layout, gather):
+    """256-row register-staged tiles (K >= 1024) with every kind of ragged
+    last tile: more or fewer than 128 rows, a single row, exact multiples of
+    the tile and empty experts."""
+    from mega_moe.ops import _kernels as K
+    counts = [518, 326, 129, 128, 65, 64, 1, 0, 300, 512, 256, 70]
+    E, N, Kd = len(counts), 512, 1024
+    offs = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32, device=DEV)
+    M = int(offs[-1])
+    g = torch.Generator(device=DEV).manual_seed(5)
+    src_rows = M + 11
+    a = torch.randn(src_rows, Kd, device=DEV, generator=g).to(torch.bfloat16)
+    a_rows = torch.randperm(src_rows, device=DEV, generator=g)[:M].to(torch.int32) if gather else None
+    if not gather:
+        a = a[:M]
+    if layout == "kcontig":
+        bt = torch.randn(E, N, Kd, device=DEV, generator=g).to(torch.bfloat16)
+        c = K.grouped_gemm(a, a_rows, bt, bt.stride(0), bt.stride(1), bt.stride(2), offs, M, N, Kd)
+        bmat = bt.transpose(1, 2)
+    else:
+        bm = torch.randn(E, Kd, N, device=DEV, generator=g).to(torch.bfloat16)
+        c = K.grouped_gemm(a, a_rows, bm, bm.stride(0), bm.stride(2), bm.stride(1), offs, M, N, Kd)
+        bmat = bm
+    torch.cuda.synchronize()
+    ref = _ref_rows_gemm(a, a_rows, bmat, offs)
+    assert_rel(c[:M], ref, 1e-2, "grouped_gemm")
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "fp8"])
+def test_fc1_ragged_tails(fmt):
+    """FC1 + gated epilogue (and the FP8 save) on the 256-row register-staged
+    tiles with every kind of ragged last tile, against a torch fp32
+    reference of gate / up and the weighted activation."""
+    from mega_moe.ops import _kernels as K
+    counts = [518, 326, 129, 128, 65, 64, 1, 0, 300, 70]
+    E, H, I = len(counts), 1024, 256
+    offs = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32, device=DEV)
+    M = int(offs[-1])
+    g = torch.Generator(device=DEV).manual_seed(6)
+    T = M // 3 + 1
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16)
+    send_token = torch.randint(0, T, (M,), device=DEV, dtype=torch.int32, generator=g)
+    w1 = (torch.randn(E, H, 2 * I, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    wperm = torch.rand(M, device=DEV, generator=g)
+    act, fc1, scale = K.fc1_swiglu(x, send_token, w1, offs, wperm, M, "swiglu", 1.0, None, 7.0, save_fc1=True,
+                                   fc1_dtype=fmt)
+    torch.cuda.synchronize()
+    xp = x.float().cpu()[send_token.long().cpu()]
+    o = offs.cpu().tolist()
+    gu = torch.zeros(M, 2 * I)
+    for e in range(E):
+        if o[e + 1] > o[e]:
+            gu[o[e]:o[e + 1]] = xp[o[e]:o[e + 1]] @ w1[e].float().cpu()
+    gu = gu.to(torch.bfloat16).float()
+    ref_act = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:] * wperm.cpu()[:, None]
+    assert_rel(act[:M], ref_act, 2e-2, "act")
+    if fmt == "bf16":
+        assert_rel(fc1[:M], gu, 1e-2, "fc1_output")
+    else:
+        deq = (fc1[:M].float().cpu().reshape(M, -1, 128) * scale[:M].cpu()[..., None]).reshape(M, 2 * I)
+        assert_rel(deq, gu, 7e-2, "fc1_output fp8")
+
+
 @pytest.mark.parametrize("kind", ["balanced", "ragged", "skew"])
 @pytest.mark.parametrize("gather", [False, True])
 @pytest.mark.parametrize("tiling", ["wide", "tile", "large", "large_reg"])
