@@ -1486,21 +1486,17 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
     // the K-contiguous dgrads, which keep 256). BK 32 x 4 stages (4 x 40 KiB)
     // keeps three stages of weight in flight per CU instead of one 80 KiB
     // stage (Kimi-scale FC1 -4%, FC2 -6% against BK 64 x 2).
-    // The weight tiles of these 128-row (weight-streaming) launches are read
-    // once, so their LDS-DMA copies carry the non-temporal hint and do not
-    // displace the activation panels that every N tile of an expert reuses
-    // from L2 (Kimi-scale FC2 4.69 -> 4.40 ms, FC2 dgrad 4.47 -> 4.13 ms,
-    // FC1 dgrad 9.52 -> 8.98 ms, FC1 unchanged; MM_WEIGHT_NT=0 drops it).
-    const bool wnt = weight_nt();
+    // The K-contiguous weight tiles of the 128-row dgrads are read once, so
+    // their LDS-DMA copies carry the non-temporal hint and do not displace
+    // the activation panel that every N tile of an expert reuses from L2
+    // (Kimi-scale layer, one process: FC2 dgrad 4.32 -> 4.13 ms, FC1 dgrad
+    // 9.56 -> 8.96 ms; MM_WEIGHT_NT=0 drops it). For the N-contiguous FC1 /
+    // FC2 weights it is neutral in isolation and 2.5% slower in the layer.
+    const bool wnt = BLAYOUT == B_KCONTIG && weight_nt();
     bool wide = false;
     if constexpr (BLAYOUT == B_NCONTIG) {
       wide = p.n % 512 == 0;
-      if (wide) {
-        if (wnt)
-          launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512, false, 1>(p, max_rows, E, s);
-        else
-          launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
-      }
+      if (wide) launch_rows_cfg<128, 512, 32, 4, BLAYOUT, EPI, 512>(p, max_rows, E, s);
     }
     if (!wide) {
       // 8 waves: 32-row wave slabs, so rows past a small expert's count skip more MFMAs
