@@ -33,19 +33,20 @@ from . import _kernels as K
 from .forward import saved_recompute
 
 
-# Step 2 overlaps step 3 when experts average more route-capacity rows than
-# this: the FC2 weight gradient is then a long MFMA-bound launch (Skew-like
-# layer, 4096 rows per expert: step 14.85 -> 14.74 ms). At 512 rows (Qwen-like)
-# the two launches are short and the overlap measured 0.6% slower; at 192 rows
-# or fewer the weight gradient streams its output and is itself HBM-bound.
-_OVERLAP_ROWS = 1024
+# Step 2 (the gated-activation backward, HBM-bound) runs on a second stream
+# beside step 3 (the FC2 weight gradient). Whole-layer A/B in one process
+# (interleaved groups of steps): Kimi-scale 42.77 -> 42.56 and 42.81 -> 42.60
+# ms per step, Qwen-like 2.565 -> 2.553 and 2.636 -> 2.584, Skew-like 14.48
+# -> 14.46. _OVERLAP_ROWS is the route-capacity rows per expert above which
+# the overlap is used (0: always).
+_OVERLAP_ROWS = 0
 _SIDE_STREAMS: dict = {}
 
 
 def overlap_act_bwd(num_routes: int, num_experts: int) -> bool:
-    """Whether step 2 runs on a second stream beside step 3: by default when
-    experts average more than 1024 route-capacity rows;
-    ``MM_BWD_ACT_OVERLAP=0`` / ``=1`` forces it off / on."""
+    """Whether step 2 runs on a second stream beside step 3: by default
+    always (for experts averaging more than ``_OVERLAP_ROWS`` route-capacity
+    rows); ``MM_BWD_ACT_OVERLAP=0`` / ``=1`` forces it off / on."""
     env = os.environ.get("MM_BWD_ACT_OVERLAP")
     if env in ("0", "1"):
         return env == "1"

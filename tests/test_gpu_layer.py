@@ -1,6 +1,8 @@
 """Layer-level parity: FusedMoEForward / moe_backward_triton / MegaMoEFunction
 against the CPU oracle (GPU)."""
 
+import math
+
 import pytest
 import torch
 
@@ -514,12 +516,18 @@ def test_stage_timing_environment(monkeypatch):
     op = _op(spec)
     assert op.stage_timer is not None
     op.stage_timer = None                      # the backward then times itself
-    for _ in range(2):
+    for overlap in ("0", "1", "0"):
+        # with the activation backward on the second stream its time is part
+        # of fc2_wgrad and the swiglu interval is NaN (not a stale value)
+        monkeypatch.setenv("MM_BWD_ACT_OVERLAP", overlap)
         out, saved = op.forward(inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"],
                                 return_saved=True)
         mega_moe.moe_backward_triton(saved, inp["dy"])
         samples = saved["_bwd_stage_samples"]
-        assert len(samples) == 1 and len(samples[0]) == 5 and all(v > 0 for v in samples[0])
+        assert len(samples) == 1 and len(samples[0]) == 5
+        d, w2, sw, w1, c = samples[0]
+        assert all(v > 0 for v in (d, w2, w1, c))
+        assert (math.isnan(sw) if overlap == "1" else sw > 0)
 
 
 def test_stage_timing_sync_finalize():
