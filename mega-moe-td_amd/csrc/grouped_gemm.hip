@@ -1394,12 +1394,8 @@ void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) 
 // barriers (-7% time on the 128-row tiles of small experts against 4
 // waves). MM_GEMM_WAVES=4 selects 4 waves.
 int eight_waves() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("MM_GEMM_WAVES");
-    v = (e && strcmp(e, "4") == 0) ? 0 : 1;
-  }
-  return v;
+  const char* e = getenv("MM_GEMM_WAVES");  // read on every call
+  return (e && strcmp(e, "4") == 0) ? 0 : 1;
 }
 
 // 256x256 row tiles with K >= 1024: 4 waves of 128x128 with register-staged
@@ -1410,12 +1406,8 @@ int eight_waves() {
 // which run the shorter K loops (Qwen-like FC2, K = 768: 0.271 against
 // 0.280 ms) and which MM_ROWS_DMA=1 selects everywhere.
 bool rows_lds_dma() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("MM_ROWS_DMA");
-    v = (e && strcmp(e, "1") == 0) ? 1 : 0;
-  }
-  return v == 1;
+  const char* e = getenv("MM_ROWS_DMA");  // read on every call
+  return e && strcmp(e, "1") == 0;
 }
 
 // Non-temporal weight copies in the 128-row row-GEMM tiles unless
