@@ -70,14 +70,14 @@ def stage_work(spec, save_fc1: bool) -> dict:
 
 
 # kernels behind each stage (the stage's HIP-event time also holds the
-# tile-list build, and for the weight gradients the operand permute)
+# tile-list build; the weight gradients gather their rows in place)
 STAGE_KERNELS = {
     "fc1_swiglu": "grouped_rows_kernel (gated epilogue)",
     "fc2": "grouped_rows_kernel",
     "fc2_dgrad": "grouped_rows_kernel (gathered dy rows)",
     "fc1_dgrad": "grouped_rows_kernel (K-contiguous gate_up)",
-    "fc2_wgrad": "permute_kernel + wgrad_persist_kernel (small K) / grouped_wgrad_kernel (deep K)",
-    "fc1_wgrad": "permute_kernel + wgrad_persist_kernel (small K) / grouped_wgrad_kernel (deep K)",
+    "fc2_wgrad": "wgrad_persist_kernel (small K) / grouped_wgrad_kernel, wgrad_reg_kernel (deep K)",
+    "fc1_wgrad": "wgrad_persist_kernel (small K) / grouped_wgrad_kernel, wgrad_reg_kernel (deep K)",
 }
 
 # CPU-baseline sample per config: (tokens, experts). Where the layer's experts
