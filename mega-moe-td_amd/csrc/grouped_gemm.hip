@@ -1220,28 +1220,44 @@ __global__ __launch_bounds__(512) void wgrad_persist_kernel(WgradArgs a, int num
   static_assert(PTile::KPC == QTile::KPC && PTile::PER_WAVE == QTile::PER_WAVE, "one K-row split for both operands");
   constexpr int PW = PTile::PER_WAVE;
   const int cap1 = a.rows_cap > 0 ? a.rows_cap - 1 : 0;
-  int pid[PW][KPC], qid[PW][KPC];
+  int pid[PW][KPC] = {}, qid[PW][KPC] = {};
   auto load_ids = [&](const TileCursor& q) {
     const int rbase = q.r0 + q.ks * BKS;
+    if (a.p_rows) {
 #pragma unroll
-    for (int v = 0; v < PW; ++v)
+      for (int v = 0; v < PW; ++v)
 #pragma unroll
-      for (int j = 0; j < KPC; ++j) {
-        const int r = min(rbase + (v * (NT / 64) + wave) * KPC + j, cap1);
-        pid[v][j] = a.p_rows ? *(const const_i32*)(a.p_rows + r) : 0;
-        qid[v][j] = a.q_rows ? *(const const_i32*)(a.q_rows + r) : 0;
-      }
+        for (int j = 0; j < KPC; ++j)
+          pid[v][j] = *(const const_i32*)(a.p_rows + min(rbase + (v * (NT / 64) + wave) * KPC + j, cap1));
+    }
+    if (a.q_rows) {
+#pragma unroll
+      for (int v = 0; v < PW; ++v)
+#pragma unroll
+        for (int j = 0; j < KPC; ++j)
+          qid[v][j] = *(const const_i32*)(a.q_rows + min(rbase + (v * (NT / 64) + wave) * KPC + j, cap1));
+    }
   };
+  // The zero row's address is read once (a load through the GOT would
+  // otherwise be repeated, with its wait, at every stage), and each copy's
+  // address is chosen with a bitwise select: with a conditional expression
+  // the compiler branched around the address arithmetic of every copy.
+  uint64_t zrow = reinterpret_cast<uint64_t>(g_wgrad_zero_row);
+  asm volatile("" : "+s"(zrow));
   auto row_src = [&](const bf16* base, int64_t ld, bool gathered, const int (&id)[KPC], int rbase, int kv, int k0,
                      int k, int64_t col) -> const bf16* {
-    int64_t r = rbase + k;
+    int r = rbase + k;
     if (gathered) {
       int pick = id[0];
 #pragma unroll
       for (int j = 1; j < KPC; ++j) pick = (k - k0 == j) ? id[j] : pick;
       r = pick;
     }
-    return k < kv ? base + r * ld + col : g_wgrad_zero_row;
+    // row offsets fit 32 x 32 bits (ld < 2^32 is checked on the host)
+    const uint64_t d = reinterpret_cast<uint64_t>(base + col) +
+                       2ull * (static_cast<uint64_t>(static_cast<uint32_t>(r)) * static_cast<uint32_t>(ld));
+    const uint64_t m = 0ull - static_cast<uint64_t>(k >= kv);
+    return reinterpret_cast<const bf16*>(d ^ ((d ^ zrow) & m));
   };
   auto issue = [&](const TileCursor& q, int buf) {
     bf16* dst = smem + buf * STAGE;
@@ -1611,6 +1627,8 @@ extern "C" int mm_grouped_wgrad(const uint16_t* p, int64_t ldp, const int32_t* p
   MM_CHECK_ARG(n1 > 0 && n1 % 128 == 0 && n2 > 0 && n2 % 128 == 0, "mm_grouped_wgrad: n1, n2 must be multiples of 128");
   MM_CHECK_ARG(ldp % 8 == 0 && ldq % 8 == 0 && al16(p) && al16(q), "mm_grouped_wgrad: 16-byte alignment required");
   MM_CHECK_ARG(max_rows >= 0 && max_rows < (int64_t(1) << 31), "mm_grouped_wgrad: bad max_rows");
+  MM_CHECK_ARG(ldp >= 0 && ldp < (int64_t(1) << 32) && ldq >= 0 && ldq < (int64_t(1) << 32),
+               "mm_grouped_wgrad: row strides must be below 2^32 elements");
   WgradArgs a{reinterpret_cast<const bf16*>(p), ldp, p_rows, reinterpret_cast<const bf16*>(q), ldq,
               q_rows, offsets, n1, n2, reinterpret_cast<bf16*>(c), static_cast<int>(max_rows)};
   hipStream_t s = mm_hip_stream(stream);
