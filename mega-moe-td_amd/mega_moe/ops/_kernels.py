@@ -198,7 +198,7 @@ def combine_bwd(dx, route_to_send, num_tokens: int, top_k: int, dscale):
 
 
 def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str, situ_beta: float,
-               situ_linear_beta, clamp_limit: float, fc1_scale=None):
+               situ_linear_beta, clamp_limit: float, fc1_scale=None, out=None):
     """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16).
 
     ``fc1_out`` is the saved raw FC1 output in bf16, fp16 or float8_e4m3fn
@@ -214,8 +214,11 @@ def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str
                 tuple(fc1_scale.shape) != (fc1_out.shape[0], 2 * inter // _lib.FC1_SCALE_GROUP):
             raise ValueError("fp8 fc1_out needs an fp32 contiguous fc1_scale [rows, 2F // 128]")
     dev = fc1_out.device
-    dab = torch.empty(max_rows, 2 * inter, dtype=torch.bfloat16, device=dev)
-    dscale = torch.empty(max_rows, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        dab = torch.empty(max_rows, 2 * inter, dtype=torch.bfloat16, device=dev)
+        dscale = torch.empty(max_rows, dtype=torch.bfloat16, device=dev)
+    else:
+        dab, dscale = out
     lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
     _lib.call("mm_swiglu_bwd", _lib.ptr(grad_act), grad_act.stride(0), _lib.ptr(fc1_out), fc1_out.stride(0),
               _lib.FC1_FORMATS[fmt], _lib.ptr(fc1_scale if fmt == "fp8" else None), _lib.ptr(scale),

@@ -34,19 +34,21 @@ from .forward import saved_recompute
 
 
 # Step 2 (the gated-activation backward, HBM-bound) runs on a second stream
-# beside step 3 (the FC2 weight gradient). Whole-layer A/B in one process
-# (interleaved groups of steps): Kimi-scale 42.77 -> 42.56 and 42.81 -> 42.60
-# ms per step, Qwen-like 2.565 -> 2.553 and 2.636 -> 2.584, Skew-like 14.48
-# -> 14.46. _OVERLAP_ROWS is the route-capacity rows per expert above which
-# the overlap is used (0: always).
-_OVERLAP_ROWS = 0
+# beside step 3 (the FC2 weight gradient) when experts average more than
+# _OVERLAP_ROWS route-capacity rows: there the deep-K weight gradient is
+# MFMA-bound and the activation backward fills idle HBM bandwidth. Whole-layer
+# A/B in one process (interleaved groups of steps), overlap off -> on:
+# Skew-like 14.553 -> 14.507 and 14.409 -> 14.382 ms per step; Qwen-like
+# (512 rows) 2.632 -> 2.637 and 2.594 -> 2.618; Kimi-scale (73 rows, both
+# kernels HBM-bound) 41.16 -> 41.16 and 41.00 -> 41.52.
+_OVERLAP_ROWS = 1024
 _SIDE_STREAMS: dict = {}
 
 
 def overlap_act_bwd(num_routes: int, num_experts: int) -> bool:
-    """Whether step 2 runs on a second stream beside step 3: by default
-    always (for experts averaging more than ``_OVERLAP_ROWS`` route-capacity
-    rows); ``MM_BWD_ACT_OVERLAP=0`` / ``=1`` forces it off / on."""
+    """Whether step 2 runs on a second stream beside step 3: by default for
+    experts averaging more than ``_OVERLAP_ROWS`` route-capacity rows;
+    ``MM_BWD_ACT_OVERLAP=0`` / ``=1`` forces it off / on."""
     env = os.environ.get("MM_BWD_ACT_OVERLAP")
     if env in ("0", "1"):
         return env == "1"
@@ -126,16 +128,21 @@ def moe_backward_triton(saved, dy, peer_mem=None, grad_transport=None, hidden_st
         # MFMA-bound deep-K weight gradient): its waves fit in the register
         # and LDS space the GEMM's one workgroup per CU leaves free (the
         # reference's step 2 || step 3, ops/backward.py:241-271)
+        # The outputs come from the main stream's pool and are not recorded
+        # on the side stream (the main stream waits for it before any use or
+        # release): allocated on the side stream, or recorded there, dAB
+        # moved between steps and the FC1 dgrad that reads it ran 0.3-0.7 ms
+        # slower at Kimi scale (same kernel and data, one process).
         main = torch.cuda.current_stream(dy.device)
+        dab = torch.empty(R, 2 * inter, dtype=torch.bfloat16, device=dy.device)
+        dscale = torch.empty(R, dtype=torch.bfloat16, device=dy.device)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            dab, dscale = K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
-                                       fc1_scale=fc1_scale, **act_kw)
+            K.swiglu_bwd(grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, R,
+                         fc1_scale=fc1_scale, out=(dab, dscale), **act_kw)
         for t in (grad_act, saved["fc1_output"], saved["recv_weights_sorted"], offsets, fc1_scale):
             if t is not None:
                 t.record_stream(side)
-        dab.record_stream(main)
-        dscale.record_stream(main)
     if side is None:
         tm.end()
     # step 3: FC2 wgrad  dW2[e][h, f] = sum_i gco[i, h] act[i, f]
