@@ -838,8 +838,14 @@ __global__ __launch_bounds__(NT) void grouped_wgrad_kernel(WgradArgs a, int num_
   };
   auto issue = [&](int s) {
     bf16* buf = smem + (s % NST) * STAGE;
-    PTile::issue_rows(buf, [&](int v) { return a.p + static_cast<int64_t>(prow[v]) * a.ldp + pc; });
-    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) { return a.q + static_cast<int64_t>(qrow[v]) * a.ldq + qc; });
+    // one 32 x 32 -> 64-bit multiply-add per row address (strides < 2^32 are
+    // checked on the host)
+    PTile::issue_rows(buf, [&](int v) {
+      return a.p + pc + static_cast<uint64_t>(static_cast<uint32_t>(prow[v])) * static_cast<uint32_t>(a.ldp);
+    });
+    QTile::issue_rows(buf + PTile::ELEMS, [&](int v) {
+      return a.q + qc + static_cast<uint64_t>(static_cast<uint32_t>(qrow[v])) * static_cast<uint32_t>(a.ldq);
+    });
   };
 
   Mma mma;
