@@ -51,3 +51,16 @@ def test_wgrad_needs_no_workspace():
     lib = _lib.load()
     E, n1, n2 = 896, 7168, 4096
     assert [lib.mm_wgrad_workspace_bytes(r, E, n1, n2) for r in (0, 1, 4096 * 16, 16384 * 16)] == [0, 0, 0, 0]
+
+@pytest.mark.skipif(not os.path.exists(_lib.library_path()), reason="libmegamoe.so not built")
+def test_wgrad_rejects_row_strides_past_32_bits():
+    """The weight-gradient kernels form row addresses with one 32 x 32-bit
+    multiply, so the host rejects row strides of 2^32 elements or more (the
+    check runs before any device call; the pointers are never read)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)  # 16-byte aligned, never dereferenced
+    args = lambda ldp, ldq: (fake, ldp, None, fake, ldq, None, fake, 8, 1024, 256, 256, fake, None, 0, None)
+    rc = lib.mm_grouped_wgrad(*args(1 << 32, 256))
+    assert rc == -1 and b"2^32" in lib.mm_last_error()
+    rc = lib.mm_grouped_wgrad(*args(256, (1 << 32) + 8))
+    assert rc == -1 and b"2^32" in lib.mm_last_error()
