@@ -202,7 +202,8 @@ def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str
     """Gated-activation backward -> (dAB [rows, 2I] bf16, dscale [rows] bf16).
 
     ``fc1_out`` is the saved raw FC1 output in bf16, fp16 or float8_e4m3fn
-    (then with its fp32 ``fc1_scale`` [rows, 2I / 128]).
+    (then with its fp32 ``fc1_scale`` [rows, 2I / 128]). ``out`` optionally
+    supplies the two result tensors (allocated by the caller).
     """
     _check_bf16("grad_act", grad_act)
     fmt = fc1_format_of(fc1_out)
@@ -219,6 +220,11 @@ def swiglu_bwd(grad_act, fc1_out, scale, offsets, max_rows: int, activation: str
         dscale = torch.empty(max_rows, dtype=torch.bfloat16, device=dev)
     else:
         dab, dscale = out
+        if dab.dtype != torch.bfloat16 or tuple(dab.shape) != (max_rows, 2 * inter) or not dab.is_contiguous() \
+                or dscale.dtype != torch.bfloat16 or tuple(dscale.shape) != (max_rows,) or not dscale.is_contiguous() \
+                or dab.device != dev or dscale.device != dev:
+            raise ValueError(f"swiglu_bwd out must be contiguous bf16 [{max_rows}, {2 * inter}] and [{max_rows}] "
+                             "tensors on the fc1_out device")
     lbeta = float(situ_linear_beta) if situ_linear_beta is not None else 0.0
     _lib.call("mm_swiglu_bwd", _lib.ptr(grad_act), grad_act.stride(0), _lib.ptr(fc1_out), fc1_out.stride(0),
               _lib.FC1_FORMATS[fmt], _lib.ptr(fc1_scale if fmt == "fp8" else None), _lib.ptr(scale),
