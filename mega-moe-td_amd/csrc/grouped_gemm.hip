@@ -441,6 +441,7 @@ struct RowsArgs {
   int64_t ldc;
   const TileList* tl;
   int group_m;  // M tiles per grouped sweep of the N tiles
+  int xcd_mod;  // 1: M tile m runs on XCD m % 8 (its N tiles in order); 0: contiguous XCD shares
   // gated (FC1) epilogue
   const float* w;
   void* fc1_out;   // saved raw gate | up in fc1_fmt (MM_FC1_*), or null
@@ -608,10 +609,17 @@ __global__ __launch_bounds__(NT) void grouped_rows_kernel(RowsArgs p) {
 
   const int num_m = p.tl->count;
   const int num_n = p.n / BN;
-  const int l = xcd_remap(blockIdx.x, num_m * num_n);
-  if (l < 0) return;
   int mt, nt;
-  grouped_mn(l, num_m, num_n, mt, nt, p.group_m);
+  if (p.xcd_mod) {
+    const int j = blockIdx.x / kXcds;
+    mt = (j / num_n) * kXcds + static_cast<int>(blockIdx.x % kXcds);
+    nt = j % num_n;
+    if (mt >= num_m) return;
+  } else {
+    const int l = xcd_remap(blockIdx.x, num_m * num_n);
+    if (l < 0) return;
+    grouped_mn(l, num_m, num_n, mt, nt, p.group_m);
+  }
   const int4 tile = p.tl->tiles[mt];
   const int e = tile.x, row0 = tile.y, rows = tile.z - tile.y;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1397,7 +1405,8 @@ RowsCfg pick_rows_cfg(int64_t max_rows, int E, int n) {
 
 template <int BM, int BN, int BK_, int NST, int BLAYOUT, int EPI, int NT = kThreads, bool REG = false, int BPOL = 0>
 void launch_rows_cfg(const RowsArgs& p, int64_t max_rows, int E, hipStream_t s) {
-  const int64_t g = max_m_tiles(max_rows, E, BM) * (p.n / BN);
+  const int64_t mm = max_m_tiles(max_rows, E, BM);
+  const int64_t g = p.xcd_mod ? (mm + kXcds - 1) / kXcds * kXcds * (p.n / BN) : mm * (p.n / BN);
   const int grid = static_cast<int>((g + kXcds - 1) / kXcds * kXcds);
   if constexpr (EPI == EPI_GATED) {  // activation specialised at compile time
     if (p.act_kind == MM_ACT_SWIGLU)
@@ -1488,6 +1497,19 @@ int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* 
   // expert's N tiles run together, so its gathered A panel stays in L2
   // (Kimi-scale: -5% layer time against 8-deep groups)
   p.group_m = c.bm == 128 ? 1 : GROUP_M;
+  // 128-row tiles stream the weights: M tile m runs on XCD m % 8, so every
+  // XCD reads experts spread over the whole weight tensor instead of one
+  // contiguous eighth of it. Where the weights' placement made one part of
+  // the tensor slower to read, the contiguous split left some XCDs finishing
+  // late (per-workgroup clocks: XCDs 5-7 at 83-85 us per FC1-dgrad tile,
+  // 0-4 at 91-92 us); Kimi-scale layer, five processes, one-process A/B:
+  // -0.84, -0.34, -0.26, +0.03, +0.04 ms per step; alternating bench
+  // processes on a sixth box: -0.32, -0.34, -0.18 ms. MM_XCD_MOD=0 restores
+  // the contiguous split (read on every call).
+  if (c.bm == 128) {
+    const char* e = getenv("MM_XCD_MOD");
+    p.xcd_mod = !(e && strcmp(e, "0") == 0);
+  }
   if (c.bm == 256) {
     if (rows_lds_dma() || p.k < 1024)
       launch_rows_cfg<256, 256, 64, 2, BLAYOUT, EPI, 512>(p, max_rows, E, s);
