@@ -33,38 +33,40 @@ from tests._numeric import assert_rel, max_rel
 
 pytestmark = pytest.mark.gpu
 
-LIMIT = 0.05
-
-# (fuzz case, T, H, I, E, k, routing, saved FC1 format); inputs drawn with
-# make_inputs(seed=100 + case) as the fuzz did
+# (fuzz case, T, H, I, E, k, routing, saved FC1 format, clamp limit); inputs
+# drawn with make_inputs(seed=100 + case) as the fuzz did. The first two
+# failed a fuzz at limit 0.05, the third one at limit 1.5 (inside the value
+# range, where many more values sit near the limit).
 FLIP_CASES = [
-    (15, 4096, 1024, 1536, 32, 8, "zipf", "fp8"),
-    (132, 4096, 2048, 1024, 32, 8, "uniform_distinct", "bf16"),
+    (15, 4096, 1024, 1536, 32, 8, "zipf", "fp8", 0.05),
+    (132, 4096, 2048, 1024, 32, 8, "uniform_distinct", "bf16", 0.05),
+    (1534, 8192, 2048, 1024, 64, 2, "zipf", "fp8", 1.5),
 ]
 
 
-def limit_flips(gu_gpu, gu_ref, inter):
+def limit_flips(gu_gpu, gu_ref, inter, limit):
     """Elements whose clamp mask differs between the two saves: the gate
     columns by ``g <= L``, the up columns by ``|u| <= L``."""
     g1, g2 = gu_gpu[:, :inter], gu_ref[:, :inter]
     u1, u2 = gu_gpu[:, inter:], gu_ref[:, inter:]
-    return torch.cat([(g1 <= LIMIT) != (g2 <= LIMIT), (u1.abs() <= LIMIT) != (u2.abs() <= LIMIT)], dim=1)
+    return torch.cat([(g1 <= limit) != (g2 <= limit), (u1.abs() <= limit) != (u2.abs() <= limit)], dim=1)
 
 
-@pytest.mark.parametrize("case", FLIP_CASES, ids=lambda c: f"fuzz{c[0]}-T{c[1]}-H{c[2]}-I{c[3]}-E{c[4]}-{c[7]}")
+@pytest.mark.parametrize("case", FLIP_CASES,
+                         ids=lambda c: f"fuzz{c[0]}-T{c[1]}-H{c[2]}-I{c[3]}-E{c[4]}-k{c[5]}-{c[7]}-L{c[8]}")
 def test_clamp_limit_flips_explain_mismatch(case):
-    i, T, H, I, E, k, routing, fmt = case
+    i, T, H, I, E, k, routing, fmt, limit = case
     print(f"clamp flip case {case}", flush=True)
     spec = CaseSpec("fuzz", T, H, I, E, k, routing, True)
     inp = make_inputs(spec, device="cuda", seed=100 + i)
-    cfg = mega_moe.MoEForwardConfig(activation="clamp_swiglu", clamp_limit=LIMIT, save_fc1_dtype=fmt)
+    cfg = mega_moe.MoEForwardConfig(activation="clamp_swiglu", clamp_limit=limit, save_fc1_dtype=fmt)
     op = mega_moe.FusedMoEForward(None, max_tokens_per_rank=T, hidden_size=H, top_k=k, num_experts=E, config=cfg)
     x, sel, w1, w2, rw, dy = inp["x"], inp["selected"], inp["gate_up"], inp["down"], inp["rw"], inp["dy"]
     out, saved = op.forward(x, sel, w1, w2, rw, return_saved=True)
     g = mega_moe.moe_backward_triton(saved, dy, peer_mem=None)
     torch.cuda.synchronize()
     _, st = O.forward(x.cpu(), sel.cpu(), w1.cpu(), w2.cpu(), rw.cpu(), activation="clamp_swiglu",
-                      clamp_limit=LIMIT, save_fc1_dtype=fmt)
+                      clamp_limit=limit, save_fc1_dtype=fmt)
     m = int(st["tables"]["offsets"][-1])
     moved = check_saved_fc1(saved, st, m, fmt)                                        # (i)
 
@@ -74,14 +76,14 @@ def test_clamp_limit_flips_explain_mismatch(case):
     gu_gpu = O.dequantize_fc1(saved["fc1_output"][:m].cpu(),
                               None if fmt != "fp8" else saved["fc1_output_scale"][:m].cpu())
     gu_ref = O.dequantize_fc1(st["fc1_output"], st.get("fc1_output_scale"))
-    explained = limit_flips(gu_gpu, gu_ref, I)
+    explained = limit_flips(gu_gpu, gu_ref, I, limit)
     if moved is not None:
         grp = O.FC1_SCALE_GROUP
         explained |= moved.repeat_interleave(grp, dim=1)
     # (ii) "off" is the 2e-2 bar of max |a - b| / max |b|, per element
     off = (dab_gpu - dab_own).abs() > 2e-2 * float(dab_own.abs().max())
     unexplained = off & ~explained
-    print(f"  flips {int(limit_flips(gu_gpu, gu_ref, I).sum())}, mismatching elements {int(off.sum())}, "
+    print(f"  flips {int(limit_flips(gu_gpu, gu_ref, I, limit).sum())}, mismatching elements {int(off.sum())}, "
           f"unexplained {int(unexplained.sum())}", flush=True)
     assert not unexplained.any(), f"{int(unexplained.sum())} grad_fc1_output mismatches are not limit flips"
     # away from the flips, the two backwards agree to the bar
