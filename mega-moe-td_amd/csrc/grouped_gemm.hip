@@ -1491,6 +1491,12 @@ template <int BLAYOUT, int EPI>
 int run_rows(RowsArgs p, const int32_t* offsets, int64_t max_rows, int E, void* ws, hipStream_t s,
              const char* what) {
   const RowsCfg c = pick_rows_cfg(max_rows, E, p.n);
+  // the largest grid any tile configuration launches (128-row M tiles padded
+  // to a multiple of 8, 128-wide N tiles) must fit a 32-bit grid size
+  if ((max_m_tiles(max_rows, E, 128) + kXcds - 1) / kXcds * kXcds * (p.n / 128) >= (int64_t(1) << 31)) {
+    mm_set_error("%s: too many tiles for one launch", what);
+    return MM_E_ARG;
+  }
   if (int rc = launch_tiles(offsets, E, c.bm, ws, s)) return rc;
   p.tl = static_cast<const TileList*>(ws);
   // 128-row tiles (experts averaging < 256 rows, weight-streaming): one

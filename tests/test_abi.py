@@ -64,3 +64,14 @@ def test_wgrad_rejects_row_strides_past_32_bits():
     assert rc == -1 and b"2^32" in lib.mm_last_error()
     rc = lib.mm_grouped_wgrad(*args(256, (1 << 32) + 8))
     assert rc == -1 and b"2^32" in lib.mm_last_error()
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.library_path()), reason="libmegamoe.so not built")
+def test_grouped_gemm_rejects_grids_past_32_bits():
+    """A row GEMM whose largest tile grid would not fit a 32-bit launch size is
+    rejected on the host before any launch (the pointers are never read)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    max_rows, E, n, k = (1 << 31) - 1, 8, 65536, 64
+    rc = lib.mm_grouped_gemm(fake, k, None, fake, n * k, 1, n, fake, E, max_rows, n, k, fake, n, fake, 1 << 40, None)
+    assert rc == -1 and b"too many tiles" in lib.mm_last_error()
