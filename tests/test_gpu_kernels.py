@@ -163,6 +163,38 @@ def test_grouped_gemm_ragged_tails(layout, gather):
     assert_rel(c[:M], ref, 1e-2, "grouped_gemm")
 
 
+@pytest.mark.parametrize("layout", ["kcontig", "ncontig"])
+@pytest.mark.parametrize("E,N", [(13, 512), (37, 256)])
+def test_weight_streaming_xcd_mapping(layout, E, N, monkeypatch):
+    """128-row tiles (experts averaging under 96 rows) run M tile m on XCD
+    m % 8; with a tile count that is no multiple of 8 (surplus workgroups
+    exit) the result is bit-identical to the contiguous per-XCD split
+    (MM_XCD_MOD=0) and matches the fp32 reference."""
+    from mega_moe.ops import _kernels as K
+    g0 = torch.Generator().manual_seed(E)
+    counts = torch.randint(0, 140, (E,), generator=g0).tolist()
+    offs = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32, device=DEV)
+    M, Kd = int(offs[-1]), 320
+    g = torch.Generator(device=DEV).manual_seed(7)
+    a = torch.randn(M + 5, Kd, device=DEV, generator=g).to(torch.bfloat16)
+    a_rows = torch.randperm(M + 5, device=DEV, generator=g)[:M].to(torch.int32)
+    if layout == "kcontig":
+        b = torch.randn(E, N, Kd, device=DEV, generator=g).to(torch.bfloat16)
+        args = (b, b.stride(0), b.stride(1), b.stride(2))
+        bmat = b.transpose(1, 2)
+    else:
+        b = torch.randn(E, Kd, N, device=DEV, generator=g).to(torch.bfloat16)
+        args = (b, b.stride(0), b.stride(2), b.stride(1))
+        bmat = b
+    out = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MM_XCD_MOD", mode)
+        out[mode] = K.grouped_gemm(a, a_rows, *args, offs, M, N, Kd)
+    torch.cuda.synchronize()
+    assert torch.equal(out["1"][:M], out["0"][:M])
+    assert_rel(out["1"][:M], _ref_rows_gemm(a, a_rows, bmat, offs), 1e-2, "grouped_gemm")
+
+
 @pytest.mark.parametrize("fmt", ["bf16", "fp8"])
 def test_fc1_ragged_tails(fmt):
     """FC1 + gated epilogue (and the FP8 save) on the 256-row register-staged
